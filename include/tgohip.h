@@ -1,0 +1,273 @@
+/*
+ * tgohip.h -- C ABI of libtgohip.so, the MI355X (gfx950) implementation of
+ * tgo's batched forward-pass hot path.
+ *
+ * tgo (github.com/latere-ai/tgo) records its forward pass as accel operators
+ * and hands the graph to golang.design/x/accel. This library replaces that
+ * boundary for the batched path: the ops of one continuous-batching step
+ * (model/qwen3_graph.go:32-128) run as hand-written HIP kernels behind the
+ * entry points below. Each entry point names the reference interface it
+ * replaces (file:line in the reference tree).
+ *
+ * Conventions (inherited from the reference):
+ *   - Every call returns 0 on success or a negative TGOHIP_E* code; the
+ *     message naming the offending field is tgohip_last_error() (thread
+ *     local). Refusals are loud, never clamps (model/batch.go:67-125).
+ *   - Out-of-range data that the reference defines is not an error: a slot
+ *     at or past the pool capacity is a dropped write (plan.go:182-192), and
+ *     a query row past the sum of the extents is inert (its output is zero).
+ *   - Pointers documented "host" are host memory; "device" pointers are HIP
+ *     device memory on the context's device. Sizes are elements unless named
+ *     *_bytes.
+ *   - One context is one device and one stream; calls on a context are
+ *     serialised by the caller (tgo serialises under Model.mu,
+ *     model.go:114-127).
+ */
+#ifndef TGOHIP_H
+#define TGOHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define TGOHIP_OK 0
+#define TGOHIP_EINVAL (-1)   /* an argument is refused; the message names it */
+#define TGOHIP_ENOMEM (-2)   /* a device allocation failed */
+#define TGOHIP_EDEVICE (-3)  /* a HIP call failed */
+#define TGOHIP_ESTATE (-4)   /* the context is not configured for this call */
+#define TGOHIP_EEXHAUSTED (-5) /* prefix.ErrExhausted (internal/prefix/prefix.go:54) */
+#define TGOHIP_ENOSLOT (-6)  /* tgo.ErrNoSlot (scheduler.go:175) */
+
+/* Weight forms: nn.Form (nn/nn.go:118-136), plus the BASELINE int4 pack. */
+#define TGOHIP_FORM_F16 0     /* [K,N] f16 row-major */
+#define TGOHIP_FORM_I8 1      /* i8 [K,N] + f16 scale per 32 flattened elements */
+#define TGOHIP_FORM_I4_TGO 2  /* u32 codes [ceil(KN/8)], element i of a word in bits
+                                 4i..4i+3; f16 scale and f16 zero per 128 flattened
+                                 elements; w = (q - z) * s */
+#define TGOHIP_FORM_I4_SYM 3  /* symmetric int4, group 32 along K: u32 [K/8][N], word
+                                 (r,n) holds k=8r+i in bits 4i..4i+3 as q+8; f16
+                                 scales [K/32][N]; w = q * s */
+
+/* Activation / output dtypes */
+#define TGOHIP_F32 0
+#define TGOHIP_F16 1
+
+const char* tgohip_last_error(void);
+const char* tgohip_version(void);
+
+/* ---- context: replaces accel.OpenBest/Device/Queue (model.go:368-387) --- */
+typedef struct tgohip_ctx tgohip_ctx;
+
+/* Opens device `device` and creates the context's stream. NULL on failure. */
+tgohip_ctx* tgohip_open(int device);
+/* Synchronises, frees every device allocation the context owns, and closes it
+ * (close order of weights/weights.go:349-371, model.go:338-365). */
+void tgohip_close(tgohip_ctx* ctx);
+/* The stream the context launches on (a hipStream_t), for callers that time
+ * kernels with events on that stream. */
+void* tgohip_stream(tgohip_ctx* ctx);
+int tgohip_sync(tgohip_ctx* ctx);
+/* Launch on a caller's stream (a hipStream_t, e.g. torch's current stream)
+ * instead of the context's own. NULL is the device's default stream. The
+ * context's own stream is a blocking stream (ordered against the default
+ * stream); tgohip_use_own_stream returns to it. */
+int tgohip_set_stream(tgohip_ctx* ctx, void* stream);
+int tgohip_use_own_stream(tgohip_ctx* ctx);
+/* Activation precision of the projections: 0 (default) rounds the activation
+ * operand to f16 for the f16 MFMA; 1 carries the f32 activation as an f16
+ * high + low pair (two MFMAs), keeping ~22 bits of it -- tgo's f32-activation
+ * semantics (nn/blocks.go:13-21) at twice the matrix-core work. */
+int tgohip_set_precision(tgohip_ctx* ctx, int mode);
+
+/* ---- model configuration: replaces model.Config (model/config.go) -------- */
+typedef struct {
+  int32_t layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
+  float rms_eps;    /* rms_norm_eps (fixture_test.go:95) */
+  float rope_theta; /* rope_theta, bound as the f32 scalar rope_base (batch.go:507-510) */
+  int32_t block;    /* positions per KV page (blocks.go:28 CacheBlock; a parameter here) */
+} tgohip_model_cfg;
+
+int tgohip_config(tgohip_ctx* ctx, const tgohip_model_cfg* cfg);
+
+/* Uploads one weight port, as nn.Graph.Weight declares it (nn/nn.go:209-259)
+ * and weights.Load binds it (weights/weights.go:629-743, model.go:489-543).
+ * port: "embed" [V,d], "lm_head" [d,V], "<l>.wq|wk|wv|wo|wgate|wup|wdown"
+ * [K,N] already transposed and q/k-permuted. plane/scales/zeros are host
+ * memory in the form's layout (scales NULL for F16, zeros NULL unless
+ * I4_TGO). The library repacks into its device layout. The embedding may be
+ * F16 or I8 (QuantGatherRows, model/qwen3_graph.go:57-61). */
+int tgohip_weight(tgohip_ctx* ctx, const char* port, int form, int K, int N,
+                  const void* plane, const void* scales, const void* zeros);
+/* Uploads an f32 norm gain (nn/nn.go:266-274, gains.go:40-69):
+ * "<l>.attn_norm|ffn_norm" [d], "<l>.qnorm|knorm" [d_h], "final_norm" [d]. */
+int tgohip_gain(tgohip_ctx* ctx, const char* port, const float* g, int width);
+/* Synthesises every weight port on the device from a seed (random init for
+ * benchmarks; bit-identical to the CPU restatement's synthesizer). form is the
+ * projections' form; the embedding is F16 under F16 and I8 otherwise. */
+int tgohip_synth_weights(tgohip_ctx* ctx, uint64_t seed, int form, double sigma);
+
+/* Allocates the shared KV pool: K and V f16 [layers, positions, kv_heads,
+ * head_dim], zeroed (blocks.go:74-139). positions is rounded down to whole
+ * pages. */
+int tgohip_kv_alloc(tgohip_ctx* ctx, int positions);
+/* Device pointers of the K and V pools and their capacity in positions. */
+int tgohip_kv_pointers(tgohip_ctx* ctx, void** k, void** v, int* positions);
+
+/* ---- one batched step: replaces Batch.step's WriteBuffer x8 + Submit +
+ *      Wait + ReadBuffer (batch.go:384-437) -------------------------------- */
+typedef struct {
+  int32_t rows;              /* plan rows T >= sum(extents) */
+  int32_t batch;             /* B members */
+  int32_t max_pages;         /* page-table width */
+  const uint32_t* ids;       /* host [rows]        model.BatchStep.IDs */
+  const uint32_t* posq;      /* host [rows*H]      .PosQ */
+  const uint32_t* posk;      /* host [rows*H_kv]   .PosK */
+  const uint32_t* slots;     /* host [rows]        .Slots */
+  const uint32_t* lengths;   /* host [B]           .Lengths */
+  const uint32_t* extents;   /* host [B]           .Extents */
+  const uint32_t* last;      /* host [B]           .Last */
+  const uint32_t* pages;     /* host [B*max_pages] page table (batch.go:397-402) */
+} tgohip_batch_step;
+
+typedef struct {
+  double submit_ms;   /* pack + upload + enqueue (bench/bench.go:60-74 "submit") */
+  double device_ms;   /* first kernel to last kernel, HIP events ("device") */
+  double readback_ms; /* logits / token ids back to the host ("readback") */
+} tgohip_timings;
+
+/* Runs the whole forward pass for one step. logits_out: host [B,V] f32 or
+ * NULL; rows of members with extent 0 are zero. argmax_out: host [B] int32 or
+ * NULL: the greedy token per member (sample/stages.go:196-206, first strict
+ * maximum; -1 for extent 0). timings may be NULL. */
+int tgohip_step(tgohip_ctx* ctx, const tgohip_batch_step* step, float* logits_out,
+                int32_t* argmax_out, tgohip_timings* timings);
+
+/* ---- op-level entry points (isolated configs and unit parity) ----------- */
+
+/* tensor.Attention, ragged + paged + f16 cache (nn/attention.go:234-253;
+ * internal/conformance/ragged_test.go:251-257). Device pointers: q [T,H,d_h]
+ * (q_dtype), k/v [C, H_kv, d_h] f16 (one layer's pool view), out [T,H,d_h]
+ * (out_dtype). Host pointers: lengths/extents [B], pages [B*max_pages].
+ * Token i of sequence s (flat row cu_s+i) sits at position L_s-n_s+i and
+ * attends to positions 0..L_s-n_s+i; rows >= sum(extents) are written zero. */
+int tgohip_paged_attention(tgohip_ctx* ctx, const void* q, int q_dtype, int T, int H,
+                           int H_kv, int head_dim, const void* k, const void* v,
+                           int capacity, int B, const uint32_t* lengths,
+                           const uint32_t* extents, const uint32_t* pages, int max_pages,
+                           int block, float scale, void* out, int out_dtype);
+
+/* The same launch planned once and replayed `iters` times with the metadata
+ * resident (timing helper; each replay is the kernels alone). */
+int tgohip_paged_attention_replay(tgohip_ctx* ctx, const void* q, int q_dtype, int T, int H,
+                                  int H_kv, const void* k, const void* v, int capacity, int B,
+                                  const uint32_t* lengths, const uint32_t* extents,
+                                  const uint32_t* pages, int max_pages, int block, float scale,
+                                  void* out, int out_dtype, int iters);
+
+/* Uploads a weight for tgohip_linear under a handle (any form above). */
+int tgohip_weight_upload(tgohip_ctx* ctx, int form, int K, int N, const void* plane,
+                         const void* scales, const void* zeros, int* handle);
+/* Synthesises a [K,N] weight of `form` on the device under a handle, from
+ * (seed, stream) as tgohip_synth_weights does for a port. */
+int tgohip_weight_synth(tgohip_ctx* ctx, int form, int K, int N, uint64_t seed, uint64_t stream,
+                        double sigma, int* handle);
+int tgohip_weight_free(tgohip_ctx* ctx, int handle);
+
+/* nn.Linear (nn/blocks.go:22-46): y[M,N] = x[M,K] . deq(W)[K,N], f32
+ * accumulate. x device [M,K] (x_dtype), y device [M,N] (y_dtype). */
+int tgohip_linear(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M, void* y,
+                  int y_dtype);
+
+/* Dequantizes a handle's weight to f32 [K,N] on the device exactly as the
+ * host restatement does ((q - z) * s in f32). y: device [K,N] f32. */
+int tgohip_dequant(tgohip_ctx* ctx, int handle, float* y);
+/* The values the MFMA path multiplies: the dequantized weight rounded once
+ * to f16 (round to nearest even). y: device [K,N] f16. */
+int tgohip_dequant_f16(tgohip_ctx* ctx, int handle, uint16_t* y);
+
+/* ---- host-side mirrors of the reference's batched path ------------------ */
+
+/* model.NewBatchStep (model/batch.go:66-152). Members are given as
+ * concatenated tokens with per-member counts, first positions and page rows
+ * of width max_pages (pages_len[i] entries valid). Outputs are host arrays
+ * sized rows, rows*H, rows*H_kv, rows, B, B, B. */
+int tgohip_new_batch_step(int vocab, int heads, int kv_heads, int rows, int B,
+                          const int32_t* tokens, const int32_t* counts, const int32_t* first,
+                          const int32_t* pages, const int32_t* pages_len, int max_pages,
+                          int block, int capacity, uint32_t* ids, uint32_t* posq,
+                          uint32_t* posk, uint32_t* slots, uint32_t* lengths,
+                          uint32_t* extents, uint32_t* last);
+
+/* nextStep (schedule.go:80-118) over n slots described by arrays:
+ * live[n], prompt_len[n], prefilled[n]. Outputs work_slot/work_start/
+ * work_count (at most n entries; start is the prompt offset for a prefill
+ * and -1 for a decode), the entry count, and the prefill/decode totals. */
+int tgohip_next_step(int n, const int32_t* live, const int32_t* prompt_len,
+                     const int32_t* prefilled, int chunk, int rows, int32_t* work_slot,
+                     int32_t* work_start, int32_t* work_count, int32_t* n_work,
+                     int32_t* prefill, int32_t* decode);
+/* victim (schedule.go:132-150): -1 when nothing is live. */
+int tgohip_victim(int n, const int32_t* live, const int32_t* prompt_len,
+                  const int32_t* prefilled, const uint64_t* arrived);
+
+/* SHA-256 (FIPS 180-4) of a byte string: the hash the prefix chain uses
+ * (internal/prefix/hash.go:46-65). */
+int tgohip_sha256(const void* data, size_t n, uint8_t* out32);
+
+/* prefix.Pool / prefix.Lease (internal/prefix/prefix.go, lease.go). */
+typedef struct tgohip_pool tgohip_pool;
+typedef struct tgohip_lease tgohip_lease;
+tgohip_pool* tgohip_pool_new(int block, int blocks, int scope);
+void tgohip_pool_free(tgohip_pool* p);
+/* stats: acquires, hits, reused, prompt, evictions, publishes, adoptions,
+ * in_use, cached, free */
+void tgohip_pool_stats(tgohip_pool* p, int64_t* stats10);
+int tgohip_pool_acquire(tgohip_pool* p, const int32_t* ids, int n, const char* session,
+                        const char* salt, int reserve, tgohip_lease** out);
+int tgohip_lease_blocks(tgohip_lease* l, int32_t* out, int cap);
+int tgohip_lease_reused(tgohip_lease* l);
+int tgohip_lease_len(tgohip_lease* l);
+int tgohip_lease_grow(tgohip_lease* l, int n);
+int tgohip_lease_commit(tgohip_lease* l, const int32_t* ids, int n);
+int tgohip_lease_publish(tgohip_lease* l, int written);
+void tgohip_lease_release(tgohip_lease* l);
+void tgohip_lease_free(tgohip_lease* l);
+
+/* Scheduler (scheduler.go:34-397) driving tgohip_step: NewScheduler, Admit,
+ * Step, Feed, Finish, Evict. The step's logits stay on the device; Step
+ * reports per produced slot the greedy token (argmax) and whether it is
+ * sampleable (Produced.Done). */
+typedef struct tgohip_sched tgohip_sched;
+/* slots n, chunk (0 = DefaultChunk 512, schedule.go:21), reserve (> 0),
+ * max_rows per step. Requires tgohip_kv_alloc. */
+tgohip_sched* tgohip_sched_new(tgohip_ctx* ctx, int n, int chunk, int reserve, int max_rows);
+void tgohip_sched_free(tgohip_sched* s);
+int tgohip_sched_admit(tgohip_sched* s, const int32_t* prompt, int n, int reserve);
+int tgohip_sched_finish(tgohip_sched* s, int slot);
+int tgohip_sched_evict(tgohip_sched* s);
+int tgohip_sched_feed(tgohip_sched* s, int slot, int token);
+int tgohip_sched_length(tgohip_sched* s, int slot);
+/* One step. out arrays sized n: slot, token (greedy), done(0/1). Returns
+ * the count produced; prefill_tokens/decodes as StepResult reports them. */
+int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
+                      int32_t* out_done, int32_t* prefill_tokens, int32_t* decodes,
+                      tgohip_timings* t);
+
+/* ---- weight conversion at load: weights/convert.go ---------------------- */
+/* f32ToF16Bits over an array (weights/convert.go:133-180): RNE, saturate to
+ * +-65504 (counted), flush below 2^-14 keeping sign, NaN -> 0x7e00. */
+size_t tgohip_to_f16(const float* src, uint16_t* dst, size_t n);
+/* int8 quantizer, one f16 scale per 32 flattened elements (convert.go:206-217). */
+void tgohip_quantize_int8(const float* src, size_t n, int8_t* q, uint16_t* scales);
+/* int4 asymmetric quantizer in the I4_TGO layout (weights/weights.go:694-743). */
+void tgohip_quantize_int4(const float* src, size_t n, uint32_t* codes, uint16_t* scales,
+                          uint16_t* zeros);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

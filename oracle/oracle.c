@@ -1,0 +1,903 @@
+/*
+ * oracle.c -- TEST INFRASTRUCTURE, NOT PRODUCT (see oracle.h).
+ *
+ * CPU restatement of tgo's batched forward-pass arithmetic. Every function
+ * cites the reference file:line it restates. The reference is Go and its
+ * kernels live in golang.design/x/accel v0.0.0-20260905175250-168f5ed9ae76
+ * (go.mod:6), which is not vendored; where accel decides a detail this file
+ * follows tgo's own call sites, tests and float64 oracle.
+ *
+ * Parity status (what pins each function; the tests under tests/ hold the
+ * checks):
+ *   orc_f32_to_f16_bits   pinned: known bits of weights/convert_test.go:106-250,
+ *                         exhaustive agreement with IEEE RNE on the normal range
+ *                         (numpy float16) and the carve-outs (saturate, FTZ).
+ *   orc_f32_to_f16_ieee   pinned: exhaustive over all 2^32 f32 against numpy.
+ *   orc_transpose/permute pinned: convert_test.go:261-297 known answers.
+ *   orc_quantize_int8     partially pinned: scale = f16(peak/127), reconstruction
+ *                         within s/2 (weights/weights_test.go:280-288). The tie
+ *                         rule of accel quant.Int8Quantize is not visible: this
+ *                         file rounds half to even against the f16-rounded scale.
+ *   orc_quantize_int4_tgo parity unpinned at the bit level (accel
+ *                         quant.Int4Quantize is absent). Format: 8 codes per u32,
+ *                         element i of a word in bits 4i..4i+3, f16 scale and f16
+ *                         integer zero per 128 flattened elements. Pinned only by
+ *                         tgo's bound (tolerance.go:151-175) and round trips.
+ *   orc_dequant_int4_sym  the BASELINE pack (symmetric, group 32 along K), defined
+ *                         by this build; pinned by closed form on tiny inputs.
+ *   orc_*_f64             pinned: known answers of the internal/oracle test files.
+ *   orc_ragged_attention_f64 pinned: reduces to orc_attention_f64 for one
+ *                         contiguous sequence (attention_test.go known answers),
+ *                         plus the C16 probe's page walk.
+ *   orc_model_step        pinned: composed of the functions above; checked
+ *                         against a float64 referenceForward restatement
+ *                         (model/graph_rig_test.go:308-371) on a small model.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <stdio.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* seeded generators                                                         */
+/* ------------------------------------------------------------------------ */
+
+uint64_t orc_splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint64_t orc_hash3(uint64_t seed, uint64_t stream, uint64_t idx) {
+  return orc_splitmix64(orc_splitmix64(seed * 0x100000001B3ull + stream) + idx);
+}
+
+/* Irwin-Hall sum of twelve 21-bit uniforms minus six: integer arithmetic up
+ * to one exact conversion, so every machine produces the same double. */
+double orc_normal(uint64_t seed, uint64_t stream, uint64_t idx) {
+  const uint64_t m = (1ull << 21) - 1;
+  int64_t s = 0;
+  for (int j = 0; j < 4; j++) {
+    uint64_t h = orc_hash3(seed, stream, idx * 4 + (uint64_t)j);
+    s += (int64_t)(h & m) + (int64_t)((h >> 21) & m) + (int64_t)((h >> 42) & m);
+  }
+  return (double)(s - 6 * (int64_t)(1 << 21)) / (double)(1 << 21);
+}
+
+void orc_synth_normal_f32(uint64_t seed, uint64_t stream, size_t n, double sigma, float* out) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)n; i++) out[i] = (float)(orc_normal(seed, stream, (uint64_t)i) * sigma);
+}
+
+void orc_synth_normal_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)n; i++) {
+    float v = (float)(orc_normal(seed, stream, (uint64_t)i) * sigma);
+    out[i] = orc_f32_to_f16_bits(v, NULL);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* f16 (weights/convert.go:17-33,153-194)                                    */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t f32bits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static float bitsf32(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* roundShift: weights/convert.go:183-194 */
+static uint32_t round_shift(uint32_t v, uint32_t n) {
+  if (n == 0) return v;
+  uint32_t keep = v >> n, rest = v & ((1u << n) - 1), half = 1u << (n - 1);
+  if (rest > half || (rest == half && (keep & 1))) keep++;
+  return keep;
+}
+
+/* f32ToF16Bits: weights/convert.go:153-180. NaN -> 0x7e00, |x| > 65504 ->
+ * sign|0x7bff (saturated), |x| < 2^-14 -> signed zero, else RNE. */
+uint16_t orc_f32_to_f16_bits(float x, int* saturated) {
+  uint32_t b = f32bits(x);
+  uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
+  if (saturated) *saturated = 0;
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7e00;
+  float a = bitsf32(b & 0x7fffffffu);
+  if (a > 65504.0f) { if (saturated) *saturated = 1; return sign | 0x7bff; }
+  if (a < 1.0f / 16384.0f) return sign;
+  int32_t e = (int32_t)((b >> 23) & 0xff) - 127;
+  uint32_t mant = b & 0x7fffffu;
+  return (uint16_t)(sign | (uint16_t)(((uint32_t)(e + 15) << 10) + round_shift(mant, 13)));
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  if (e == 0) {
+    if (m == 0) return bitsf32(sign);
+    float v = ldexpf((float)m, -24);
+    return (h & 0x8000) ? -v : v;
+  }
+  if (e == 31) return bitsf32(sign | 0x7f800000u | (m << 13));
+  return bitsf32(sign | ((e + 112) << 23) | (m << 13));
+}
+
+/* IEEE RNE narrowing (the device Cast of nn/attention.go:227-230). */
+uint16_t orc_f32_to_f16_ieee(float x) {
+  uint32_t b = f32bits(x);
+  uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
+  uint32_t a = b & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00 | ((a >> 13) & 0x3ff));
+  if (a >= 0x477ff000u) return sign | 0x7c00; /* rounds to >= 65520 -> inf */
+  int32_t e = (int32_t)(a >> 23) - 127;
+  if (e >= -14) {
+    uint32_t mant = a & 0x7fffffu;
+    return (uint16_t)(sign | (uint16_t)(((uint32_t)(e + 15) << 10) + round_shift(mant, 13)));
+  }
+  if (e < -25) return sign; /* below half the smallest subnormal */
+  /* subnormal: value = mant24 * 2^(e-23); result units of 2^-24 */
+  uint32_t mant24 = (a & 0x7fffffu) | 0x800000u;
+  uint32_t shift = (uint32_t)(-e - 14 + 13); /* 2^(e-23) / 2^-24 = 2^(e+1) */
+  return (uint16_t)(sign | round_shift(mant24, shift));
+}
+
+/* toF16: weights/convert.go:133-143 */
+size_t orc_to_f16(const float* src, uint16_t* dst, size_t n) {
+  size_t sat = 0;
+  for (size_t i = 0; i < n; i++) { int s; dst[i] = orc_f32_to_f16_bits(src[i], &s); sat += (size_t)s; }
+  return sat;
+}
+
+/* transpose: weights/convert.go:79-86 */
+void orc_transpose(const float* src, float* dst, int rows, int cols) {
+  for (int r = 0; r < rows; r++)
+    for (int c = 0; c < cols; c++) dst[(size_t)c * rows + r] = src[(size_t)r * cols + c];
+}
+
+/* permuteHeads: weights/convert.go:106-125, y[2i]=x[i], y[2i+1]=x[i+d/2] */
+int orc_permute_heads(float* x, size_t n, int last_axis, int head_dim) {
+  if (head_dim <= 0 || head_dim % 2 != 0) return -1;
+  if (last_axis % head_dim != 0) return -2;
+  int half = head_dim / 2;
+  float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+  for (size_t off = 0; off + (size_t)head_dim <= n; off += (size_t)head_dim) {
+    memcpy(tmp, x + off, sizeof(float) * (size_t)head_dim);
+    for (int i = 0; i < half; i++) { x[off + 2 * i] = tmp[i]; x[off + 2 * i + 1] = tmp[i + half]; }
+  }
+  free(tmp);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantized forms                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* round half to even on a double */
+static double rne(double v) {
+  double r = nearbyint(v); /* default rounding mode is to-nearest-even */
+  return r;
+}
+
+/* int8: one f16 scale per 32 consecutive flattened elements, scale =
+ * peak/127 (weights/convert.go:196-219, weights/weights_test.go:280-288). */
+void orc_quantize_int8(const float* w, size_t n, int8_t* q, uint16_t* scales) {
+  for (size_t lo = 0; lo < n; lo += 32) {
+    size_t hi = lo + 32 < n ? lo + 32 : n;
+    float peak = 0;
+    for (size_t i = lo; i < hi; i++) { float a = fabsf(w[i]); if (a > peak) peak = a; }
+    uint16_t s16 = orc_f32_to_f16_bits(peak / 127.0f, NULL);
+    float s = orc_f16_to_f32(s16);
+    scales[lo / 32] = s16;
+    for (size_t i = lo; i < hi; i++) {
+      double v = s > 0 ? rne((double)w[i] / (double)s) : 0.0;
+      if (v > 127) v = 127;
+      if (v < -127) v = -127;
+      q[i] = (int8_t)v;
+    }
+  }
+}
+
+void orc_dequant_int8(const int8_t* q, const uint16_t* scales, size_t n, float* out) {
+  for (size_t i = 0; i < n; i++) out[i] = (float)q[i] * orc_f16_to_f32(scales[i / 32]);
+}
+
+/* int4, tgo layout (nn/nn.go:128-135,315-333; tolerance.go:151-160): codes in
+ * u32 words, element i of word w is bits 4i..4i+3 of word w; one f16 scale and
+ * one f16 zero per 128 flattened elements; w = (q - z) * s. This build's
+ * quantizer: s = f16((max-min)/15) (1 when the group is flat), z = f16(an
+ * integer in [0,15]) = round(-min/s) clamped, q = clamp(round(x/s + z), 0, 15). */
+void orc_quantize_int4_tgo(const float* w, size_t n, uint32_t* codes, uint16_t* scales,
+                           uint16_t* zeros) {
+  size_t words = (n + 7) / 8;
+  memset(codes, 0, words * 4);
+  for (size_t lo = 0; lo < n; lo += 128) {
+    size_t hi = lo + 128 < n ? lo + 128 : n;
+    float mn = w[lo], mx = w[lo];
+    for (size_t i = lo; i < hi; i++) { if (w[i] < mn) mn = w[i]; if (w[i] > mx) mx = w[i]; }
+    float sr = (mx - mn) / 15.0f;
+    uint16_t s16 = orc_f32_to_f16_bits(sr > 0 ? sr : 1.0f, NULL);
+    float s = orc_f16_to_f32(s16);
+    if (s == 0) { s16 = 0x3c00; s = 1.0f; }
+    double zf = rne(-(double)mn / (double)s);
+    if (zf < 0) zf = 0;
+    if (zf > 15) zf = 15;
+    uint16_t z16 = orc_f32_to_f16_bits((float)zf, NULL);
+    scales[lo / 128] = s16;
+    zeros[lo / 128] = z16;
+    for (size_t i = lo; i < hi; i++) {
+      double v = rne((double)w[i] / (double)s + zf);
+      if (v < 0) v = 0;
+      if (v > 15) v = 15;
+      codes[i / 8] |= ((uint32_t)v & 15u) << (4 * (i % 8));
+    }
+  }
+}
+
+void orc_dequant_int4_tgo(const uint32_t* codes, const uint16_t* scales, const uint16_t* zeros,
+                          size_t n, float* out) {
+  for (size_t i = 0; i < n; i++) {
+    uint32_t q = (codes[i / 8] >> (4 * (i % 8))) & 15u;
+    float s = orc_f16_to_f32(scales[i / 128]), z = orc_f16_to_f32(zeros[i / 128]);
+    out[i] = ((float)q - z) * s;
+  }
+}
+
+/* Int4ErrorBound restated over stored scale/zero (tolerance.go:160,
+ * reaudit_test.go:283-293): (1/30) sum |x_p| * (range of group(p,col)),
+ * the range being 15*s of the stored scale. */
+double orc_int4_tgo_bound(const float* x, const uint16_t* scales, const uint16_t* zeros,
+                          int k, int n, int col) {
+  (void)zeros;
+  double b = 0;
+  for (int p = 0; p < k; p++) {
+    size_t g = ((size_t)p * (size_t)n + (size_t)col) / 128;
+    double range = 15.0 * (double)orc_f16_to_f32(scales[g]);
+    b += fabs((double)x[p]) * range;
+  }
+  return b / 30.0;
+}
+
+/* The BASELINE pack: symmetric int4, group 32 along K. qweight is [K/8][N]
+ * u32, word (r, n) holds k = 8r..8r+7 with k = 8r+i in bits 4i..4i+3 as the
+ * unsigned nibble q+8; scales [K/32][N] f16; w[k][n] = q * s[k/32][n]. */
+void orc_dequant_int4_sym(const uint32_t* qweight, const uint16_t* scales, int K, int N,
+                          float* out) {
+  for (int k = 0; k < K; k++)
+    for (int n = 0; n < N; n++) {
+      uint32_t u = (qweight[(size_t)(k / 8) * N + n] >> (4 * (k % 8))) & 15u;
+      float s = orc_f16_to_f32(scales[(size_t)(k / 32) * N + n]);
+      out[(size_t)k * N + n] = (float)((int)u - 8) * s;
+    }
+}
+
+void orc_synth_int4_sym(uint64_t seed, uint64_t stream, int K, int N, double sigma,
+                        uint32_t* qweight, uint16_t* scales) {
+#pragma omp parallel for schedule(static)
+  for (long long r = 0; r < (long long)(K / 8); r++)
+    for (int n = 0; n < N; n++) {
+      uint32_t word = 0;
+      for (int i = 0; i < 8; i++) {
+        uint64_t e = (uint64_t)(r * 8 + i) * (uint64_t)N + (uint64_t)n;
+        word |= (uint32_t)(orc_hash3(seed, stream * 4 + 0, e) & 15u) << (4 * i);
+      }
+      qweight[(size_t)r * N + n] = word;
+    }
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)(K / 32) * N; i++) {
+    float v = (float)(fabs(orc_normal(seed, stream * 4 + 1, (uint64_t)i)) * sigma);
+    scales[i] = orc_f32_to_f16_bits(v, NULL);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* float64 oracle: internal/oracle/oracle.go, attention.go, rope.go          */
+/* ------------------------------------------------------------------------ */
+
+/* RMSNorm: internal/oracle/oracle.go:45-67 */
+void orc_rmsnorm_f64(const double* x, const double* gain, int rows, int width, double eps,
+                     double* out) {
+  for (int r = 0; r < rows; r++) {
+    const double* row = x + (size_t)r * width;
+    double sum = 0;
+    for (int c = 0; c < width; c++) sum += row[c] * row[c];
+    double scale = 1.0 / sqrt(sum / (double)width + eps);
+    for (int c = 0; c < width; c++) out[(size_t)r * width + c] = row[c] * scale * gain[c];
+  }
+}
+
+/* MatMul: internal/oracle/oracle.go:78-99 */
+void orc_matmul_f64(const double* x, const double* w, int m, int k, int n, double* out) {
+  for (int i = 0; i < m; i++)
+    for (int j = 0; j < n; j++) {
+      double s = 0;
+      for (int p = 0; p < k; p++) s += x[(size_t)i * k + p] * w[(size_t)p * n + j];
+      out[(size_t)i * n + j] = s;
+    }
+}
+
+/* SiLU / SwiGLU: internal/oracle/oracle.go:106-129 */
+void orc_silu_f64(const double* x, int n, double* out) {
+  for (int i = 0; i < n; i++) out[i] = x[i] / (1.0 + exp(-x[i]));
+}
+void orc_swiglu_f64(const double* gate, const double* up, int n, double* out) {
+  orc_silu_f64(gate, n, out);
+  for (int i = 0; i < n; i++) out[i] *= up[i];
+}
+
+/* Softmax: internal/oracle/oracle.go:137-158 */
+void orc_softmax_f64(const double* x, int n, double* out) {
+  double mx = -INFINITY, sum = 0;
+  for (int i = 0; i < n; i++) if (x[i] > mx) mx = x[i];
+  for (int i = 0; i < n; i++) { out[i] = exp(x[i] - mx); sum += out[i]; }
+  for (int i = 0; i < n; i++) out[i] /= sum;
+}
+
+/* GatherRows: internal/oracle/oracle.go:168-183 */
+void orc_gather_rows_f64(const double* table, int vocab, int width, const int* ids, int n,
+                         double* out) {
+  (void)vocab;
+  for (int i = 0; i < n; i++)
+    memcpy(out + (size_t)i * width, table + (size_t)ids[i] * width, sizeof(double) * (size_t)width);
+}
+
+/* RoPE: internal/oracle/rope.go:83-146. style 1 = interleaved, 2 = half-split. */
+void orc_rope_f64(const double* x, int rows, int width, int rotary, double base,
+                  const int* pos, int style, double* out) {
+  memcpy(out, x, sizeof(double) * (size_t)rows * (size_t)width);
+  int half = rotary / 2;
+  for (int r = 0; r < rows; r++) {
+    double m = (double)pos[r];
+    for (int i = 0; i < half; i++) {
+      double angle = m * pow(base, -2.0 * (double)i / (double)rotary);
+      double s = sin(angle), c = cos(angle);
+      int lo = style == 1 ? 2 * i : i, hi = style == 1 ? 2 * i + 1 : i + half;
+      double lv = out[(size_t)r * width + lo], hv = out[(size_t)r * width + hi];
+      out[(size_t)r * width + lo] = lv * c - hv * s;
+      out[(size_t)r * width + hi] = lv * s + hv * c;
+    }
+  }
+}
+
+/* Attention: internal/oracle/attention.go:39-95 */
+void orc_attention_f64(const double* q, const double* k, const double* v, int qseq, int qheads,
+                       int kvheads, int headdim, int kvlen, double scale, int causal_base,
+                       double* out) {
+  (void)kvlen;
+  int group = qheads / kvheads;
+  memset(out, 0, sizeof(double) * (size_t)qseq * qheads * headdim);
+  for (int t = 0; t < qseq; t++) {
+    int visible = causal_base + t + 1;
+    double* scores = (double*)malloc(sizeof(double) * (size_t)visible);
+    double* w = (double*)malloc(sizeof(double) * (size_t)visible);
+    for (int h = 0; h < qheads; h++) {
+      int kvh = h / group;
+      const double* qrow = q + ((size_t)t * qheads + h) * headdim;
+      for (int j = 0; j < visible; j++) {
+        const double* krow = k + ((size_t)j * kvheads + kvh) * headdim;
+        double dot = 0;
+        for (int c = 0; c < headdim; c++) dot += qrow[c] * krow[c];
+        scores[j] = dot * scale;
+      }
+      orc_softmax_f64(scores, visible, w);
+      double* orow = out + ((size_t)t * qheads + h) * headdim;
+      for (int j = 0; j < visible; j++) {
+        const double* vrow = v + ((size_t)j * kvheads + kvh) * headdim;
+        for (int c = 0; c < headdim; c++) orow[c] += w[j] * vrow[c];
+      }
+    }
+    free(scores);
+    free(w);
+  }
+}
+
+/* raggedOracle: internal/conformance/ragged_test.go:151-208. Token i of
+ * sequence s sits at position L_s - n_s + i and attends to positions
+ * 0..L_s-n_s+i through the page table; query head h reads kv head
+ * h/(H/Hkv). The cache is either f16 (k_f16/v_f16) or f32. budget3 receives
+ * {max|v| attended, max|score|, max positions} (ragged_test.go:140-149).
+ * Rows past the extents are left at zero. */
+void orc_ragged_attention_f64(const float* q, int T, int H, int Hkv, int dh,
+                              const uint16_t* k_f16, const uint16_t* v_f16,
+                              const float* k_f32, const float* v_f32,
+                              int B, const uint32_t* lengths, const uint32_t* extents,
+                              const uint32_t* pages, int max_pages, int block, double scale,
+                              double* out, double* budget3) {
+  int group = H / Hkv;
+  double bv = 0, bs = 0, bp = 0;
+  memset(out, 0, sizeof(double) * (size_t)T * H * dh);
+  int tok = 0;
+  for (int s = 0; s < B; s++) {
+    int n = (int)extents[s], L = (int)lengths[s];
+    for (int i = 0; i < n; i++, tok++) {
+      if (tok >= T) break;
+      int limit = L - n + i;
+      double* scores = (double*)malloc(sizeof(double) * (size_t)(limit + 1));
+      for (int h = 0; h < H; h++) {
+        int kvh = h / group;
+        double mx = -INFINITY;
+        for (int p = 0; p <= limit; p++) {
+          size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+          double dot = 0;
+          for (int d = 0; d < dh; d++) {
+            double qv = q[((size_t)tok * H + h) * dh + d];
+            size_t ki = (row * Hkv + kvh) * dh + d;
+            double kv = k_f16 ? orc_f16_to_f32(k_f16[ki]) : k_f32[ki];
+            dot += qv * kv;
+          }
+          scores[p] = dot * scale;
+          if (scores[p] > mx) mx = scores[p];
+          if (fabs(scores[p]) > bs) bs = fabs(scores[p]);
+        }
+        if (limit + 1 > bp) bp = limit + 1;
+        double sum = 0;
+        for (int p = 0; p <= limit; p++) { scores[p] = exp(scores[p] - mx); sum += scores[p]; }
+        for (int d = 0; d < dh; d++) {
+          double acc = 0;
+          for (int p = 0; p <= limit; p++) {
+            size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+            size_t vi = (row * Hkv + kvh) * dh + d;
+            double val = v_f16 ? orc_f16_to_f32(v_f16[vi]) : v_f32[vi];
+            acc += scores[p] * val;
+            if (fabs(val) > bv) bv = fabs(val);
+          }
+          out[((size_t)tok * H + h) * dh + d] = acc / sum;
+        }
+      }
+      free(scores);
+    }
+  }
+  if (budget3) { budget3[0] = bv; budget3[1] = bs; budget3[2] = bp; }
+}
+
+/* ------------------------------------------------------------------------ */
+/* f32 CPU path                                                              */
+/* ------------------------------------------------------------------------ */
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* The f32 CPU path's ragged attention: f16 cache widened to f32, f32 scores,
+ * f32 max-subtracted softmax, f32 accumulation; same semantics as
+ * orc_ragged_attention_f64 (ragged_test.go:151-208). */
+void orc_cpu_ragged_attention(const float* q, int T, int H, int Hkv, int dh,
+                              const uint16_t* kc, const uint16_t* vc, int B,
+                              const uint32_t* lengths, const uint32_t* extents,
+                              const uint32_t* pages, int max_pages, int block, float scale,
+                              float* out) {
+  int group = H / Hkv;
+  int* seq_of = (int*)malloc(sizeof(int) * (size_t)(T > 0 ? T : 1));
+  int* idx_of = (int*)malloc(sizeof(int) * (size_t)(T > 0 ? T : 1));
+  int tok = 0;
+  for (int s = 0; s < B; s++)
+    for (int i = 0; i < (int)extents[s] && tok < T; i++, tok++) { seq_of[tok] = s; idx_of[tok] = i; }
+  int claimed = tok;
+  memset(out, 0, sizeof(float) * (size_t)T * H * dh);
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+  for (int t = 0; t < claimed; t++)
+    for (int h = 0; h < H; h++) {
+      int s = seq_of[t], n = (int)extents[s], L = (int)lengths[s];
+      int limit = L - n + idx_of[t];
+      int kvh = h / group;
+      float* sc = (float*)malloc(sizeof(float) * (size_t)(limit + 1));
+      const float* qr = q + ((size_t)t * H + h) * dh;
+      float mx = -INFINITY;
+      for (int p = 0; p <= limit; p++) {
+        size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+        const uint16_t* kr = kc + (row * Hkv + kvh) * dh;
+        float dot = 0;
+        for (int d = 0; d < dh; d++) dot += qr[d] * orc_f16_to_f32(kr[d]);
+        sc[p] = dot * scale;
+        if (sc[p] > mx) mx = sc[p];
+      }
+      float sum = 0;
+      for (int p = 0; p <= limit; p++) { sc[p] = expf(sc[p] - mx); sum += sc[p]; }
+      float* o = out + ((size_t)t * H + h) * dh;
+      for (int p = 0; p <= limit; p++) {
+        size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+        const uint16_t* vr = vc + (row * Hkv + kvh) * dh;
+        for (int d = 0; d < dh; d++) o[d] += sc[p] * orc_f16_to_f32(vr[d]);
+      }
+      for (int d = 0; d < dh; d++) o[d] /= sum;
+      free(sc);
+    }
+  free(seq_of);
+  free(idx_of);
+}
+
+/* dequantize one K row (k) of a [K,N] weight into dst[N] as f32 */
+static void deq_row(int form, const void* plane, const void* scales, const void* zeros, int K,
+                    int N, int k, float* dst) {
+  (void)K;
+  size_t base = (size_t)k * N;
+  switch (form) {
+    case ORC_FORM_F16: {
+      const uint16_t* w = (const uint16_t*)plane;
+      for (int n = 0; n < N; n++) dst[n] = orc_f16_to_f32(w[base + n]);
+    } break;
+    case ORC_FORM_I8: {
+      const int8_t* q = (const int8_t*)plane;
+      const uint16_t* s = (const uint16_t*)scales;
+      for (int n = 0; n < N; n++) dst[n] = (float)q[base + n] * orc_f16_to_f32(s[(base + n) / 32]);
+    } break;
+    case ORC_FORM_I4_TGO: {
+      const uint32_t* c = (const uint32_t*)plane;
+      const uint16_t* s = (const uint16_t*)scales;
+      const uint16_t* z = (const uint16_t*)zeros;
+      for (int n = 0; n < N; n++) {
+        size_t i = base + n;
+        uint32_t qv = (c[i / 8] >> (4 * (i % 8))) & 15u;
+        dst[n] = ((float)qv - orc_f16_to_f32(z[i / 128])) * orc_f16_to_f32(s[i / 128]);
+      }
+    } break;
+    case ORC_FORM_I4_SYM: {
+      const uint32_t* c = (const uint32_t*)plane;
+      const uint16_t* s = (const uint16_t*)scales;
+      for (int n = 0; n < N; n++) {
+        uint32_t u = (c[(size_t)(k / 8) * N + n] >> (4 * (k % 8))) & 15u;
+        dst[n] = (float)((int)u - 8) * orc_f16_to_f32(s[(size_t)(k / 32) * N + n]);
+      }
+    } break;
+  }
+}
+
+/* Linear, f32 path: y = x deq(W), f32 accumulation in k order
+ * (nn/blocks.go:22-46; internal/oracle/oracle.go:78-99). Parallel over
+ * output columns in blocks; each block dequantizes a K-row slice once. */
+int orc_cpu_linear(const float* x, int M, int K, int N, int form, const void* plane,
+                   const void* scales, const void* zeros, float* y) {
+  const int NB = 256;
+  int nblk = (N + NB - 1) / NB;
+#pragma omp parallel
+  {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)N);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)M * NB);
+#pragma omp for schedule(dynamic, 1)
+    for (int b = 0; b < nblk; b++) {
+      int n0 = b * NB, n1 = n0 + NB < N ? n0 + NB : N, w = n1 - n0;
+      memset(acc, 0, sizeof(float) * (size_t)M * NB);
+      for (int k = 0; k < K; k++) {
+        /* dequantize only this block's columns */
+        switch (form) {
+          case ORC_FORM_I4_SYM: {
+            const uint32_t* c = (const uint32_t*)plane;
+            const uint16_t* s = (const uint16_t*)scales;
+            for (int n = n0; n < n1; n++) {
+              uint32_t u = (c[(size_t)(k / 8) * N + n] >> (4 * (k % 8))) & 15u;
+              wrow[n] = (float)((int)u - 8) * orc_f16_to_f32(s[(size_t)(k / 32) * N + n]);
+            }
+          } break;
+          default: {
+            /* generic: dequantize the row segment */
+            size_t base = (size_t)k * N;
+            for (int n = n0; n < n1; n++) {
+              size_t i = base + n;
+              if (form == ORC_FORM_F16) wrow[n] = orc_f16_to_f32(((const uint16_t*)plane)[i]);
+              else if (form == ORC_FORM_I8)
+                wrow[n] = (float)((const int8_t*)plane)[i] * orc_f16_to_f32(((const uint16_t*)scales)[i / 32]);
+              else {
+                uint32_t qv = (((const uint32_t*)plane)[i / 8] >> (4 * (i % 8))) & 15u;
+                wrow[n] = ((float)qv - orc_f16_to_f32(((const uint16_t*)zeros)[i / 128])) *
+                          orc_f16_to_f32(((const uint16_t*)scales)[i / 128]);
+              }
+            }
+          } break;
+        }
+        for (int m = 0; m < M; m++) {
+          float xv = x[(size_t)m * K + k];
+          float* a = acc + (size_t)m * NB;
+          for (int n = 0; n < w; n++) a[n] += xv * wrow[n0 + n];
+        }
+      }
+      for (int m = 0; m < M; m++) memcpy(y + (size_t)m * N + n0, acc + (size_t)m * NB, sizeof(float) * (size_t)w);
+    }
+    free(wrow);
+    free(acc);
+  }
+  return 0;
+}
+
+typedef struct {
+  int form, K, N;
+  void* plane;
+  void* scales;
+  void* zeros;
+} orc_weight;
+
+enum { P_ATTN_NORM, P_WQ, P_WK, P_WV, P_WO, P_QNORM, P_KNORM, P_FFN_NORM, P_WGATE, P_WUP, P_WDOWN, P_NLAYER };
+static const char* layer_ports[P_NLAYER] = {"attn_norm", "wq", "wk", "wv", "wo", "qnorm",
+                                            "knorm", "ffn_norm", "wgate", "wup", "wdown"};
+
+struct orc_model {
+  int L, d, H, Hkv, dh, f, V, block, C;
+  float eps, theta;
+  orc_weight embed, lm_head;
+  float* final_norm;
+  orc_weight* lw;  /* [L][P_NLAYER] (gain entries unused) */
+  float** gains;   /* [L][P_NLAYER] (only gain ports used) */
+  uint16_t* kc;    /* [L][C][Hkv][dh] f16 */
+  uint16_t* vc;
+};
+
+orc_model* orc_model_new(int layers, int hidden, int heads, int kv_heads, int head_dim, int ffn,
+                         int vocab, float eps, float theta, int block, int capacity) {
+  orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+  m->L = layers; m->d = hidden; m->H = heads; m->Hkv = kv_heads; m->dh = head_dim;
+  m->f = ffn; m->V = vocab; m->eps = eps; m->theta = theta; m->block = block; m->C = capacity;
+  m->lw = (orc_weight*)calloc((size_t)layers * P_NLAYER, sizeof(orc_weight));
+  m->gains = (float**)calloc((size_t)layers * P_NLAYER, sizeof(float*));
+  size_t kvn = (size_t)layers * capacity * kv_heads * head_dim;
+  m->kc = (uint16_t*)calloc(kvn, 2);
+  m->vc = (uint16_t*)calloc(kvn, 2);
+  return m;
+}
+
+static void free_weight(orc_weight* w) { free(w->plane); free(w->scales); free(w->zeros); }
+
+void orc_model_free(orc_model* m) {
+  if (!m) return;
+  free_weight(&m->embed);
+  free_weight(&m->lm_head);
+  free(m->final_norm);
+  for (int i = 0; i < m->L * P_NLAYER; i++) { free_weight(&m->lw[i]); free(m->gains[i]); }
+  free(m->lw); free(m->gains); free(m->kc); free(m->vc);
+  free(m);
+}
+
+void orc_model_kv(orc_model* m, uint16_t** k, uint16_t** v) { *k = m->kc; *v = m->vc; }
+
+static size_t plane_bytes(int form, int K, int N) {
+  size_t n = (size_t)K * N;
+  switch (form) {
+    case ORC_FORM_F16: return n * 2;
+    case ORC_FORM_I8: return n;
+    case ORC_FORM_I4_TGO: return (n + 7) / 8 * 4;
+    case ORC_FORM_I4_SYM: return n / 2;
+  }
+  return 0;
+}
+static size_t scale_count(int form, int K, int N) {
+  size_t n = (size_t)K * N;
+  switch (form) {
+    case ORC_FORM_I8: return (n + 31) / 32;
+    case ORC_FORM_I4_TGO: return (n + 127) / 128;
+    case ORC_FORM_I4_SYM: return (size_t)(K / 32) * N;
+  }
+  return 0;
+}
+
+static void set_weight(orc_weight* w, int form, int K, int N, const void* plane,
+                       const void* scales, const void* zeros) {
+  free_weight(w);
+  w->form = form; w->K = K; w->N = N;
+  size_t pb = plane_bytes(form, K, N), sc = scale_count(form, K, N);
+  w->plane = malloc(pb);
+  memcpy(w->plane, plane, pb);
+  w->scales = w->zeros = NULL;
+  if (sc) { w->scales = malloc(sc * 2); memcpy(w->scales, scales, sc * 2); }
+  if (form == ORC_FORM_I4_TGO) { w->zeros = malloc(sc * 2); memcpy(w->zeros, zeros, sc * 2); }
+}
+
+int orc_model_weight(orc_model* m, const char* port, int form, int K, int N, const void* plane,
+                     const void* scales, const void* zeros) {
+  if (!strcmp(port, "embed")) { set_weight(&m->embed, form, K, N, plane, scales, zeros); return 0; }
+  if (!strcmp(port, "lm_head")) { set_weight(&m->lm_head, form, K, N, plane, scales, zeros); return 0; }
+  int l, off;
+  if (sscanf(port, "%d.%n", &l, &off) != 1 || l < 0 || l >= m->L) return -1;
+  for (int p = 0; p < P_NLAYER; p++)
+    if (!strcmp(port + off, layer_ports[p])) {
+      set_weight(&m->lw[l * P_NLAYER + p], form, K, N, plane, scales, zeros);
+      return 0;
+    }
+  return -1;
+}
+
+int orc_model_gain(orc_model* m, const char* port, const float* g, int width) {
+  float* c = (float*)malloc(sizeof(float) * (size_t)width);
+  memcpy(c, g, sizeof(float) * (size_t)width);
+  if (!strcmp(port, "final_norm")) { free(m->final_norm); m->final_norm = c; return 0; }
+  int l, off;
+  if (sscanf(port, "%d.%n", &l, &off) != 1 || l < 0 || l >= m->L) { free(c); return -1; }
+  for (int p = 0; p < P_NLAYER; p++)
+    if (!strcmp(port + off, layer_ports[p])) {
+      free(m->gains[l * P_NLAYER + p]);
+      m->gains[l * P_NLAYER + p] = c;
+      return 0;
+    }
+  free(c);
+  return -1;
+}
+
+/* Synthetic weights (the definition the product's synthesizer restates on
+ * the device): stream ids are 1 embed, 2 final_norm, 3 lm_head, and
+ * (l+1)*64+p for layer ports; sub-streams stream*4+{0 codes,1 scales,2 zeros}.
+ *   F16:     N(0,sigma) narrowed by the loader rule (f32ToF16Bits).
+ *   I8:      q = hash%255-127, s = f16(|N|*sigma/64).
+ *   I4_TGO:  q = hash&15, s = f16(|N|*sigma/4), z = 7 + (hash&1).
+ *   I4_SYM:  q = hash&15 (nibble = q+8 convention), s = f16(|N|*sigma/4).
+ * Gains are 1.0. Under int4 the embedding is int8 (weights/weights.go:543-545). */
+static void synth_weight(orc_weight* w, uint64_t seed, uint64_t stream, int form, int K, int N,
+                         double sigma) {
+  free_weight(w);
+  w->form = form; w->K = K; w->N = N;
+  size_t n = (size_t)K * N;
+  size_t pb = plane_bytes(form, K, N), sc = scale_count(form, K, N);
+  w->plane = malloc(pb);
+  w->scales = sc ? malloc(sc * 2) : NULL;
+  w->zeros = form == ORC_FORM_I4_TGO ? malloc(sc * 2) : NULL;
+  switch (form) {
+    case ORC_FORM_F16: orc_synth_normal_f16(seed, stream * 4, n, sigma, (uint16_t*)w->plane); break;
+    case ORC_FORM_I8: {
+      int8_t* q = (int8_t*)w->plane;
+#pragma omp parallel for schedule(static)
+      for (long long i = 0; i < (long long)n; i++)
+        q[i] = (int8_t)((int)(orc_hash3(seed, stream * 4, (uint64_t)i) % 255u) - 127);
+      uint16_t* s = (uint16_t*)w->scales;
+#pragma omp parallel for schedule(static)
+      for (long long i = 0; i < (long long)sc; i++)
+        s[i] = orc_f32_to_f16_bits((float)(fabs(orc_normal(seed, stream * 4 + 1, (uint64_t)i)) * sigma / 64.0), NULL);
+    } break;
+    case ORC_FORM_I4_TGO: {
+      uint32_t* c = (uint32_t*)w->plane;
+      size_t words = (n + 7) / 8;
+#pragma omp parallel for schedule(static)
+      for (long long wi = 0; wi < (long long)words; wi++) {
+        uint32_t word = 0;
+        for (int i = 0; i < 8; i++) {
+          size_t e = (size_t)wi * 8 + (size_t)i;
+          if (e < n) word |= (uint32_t)(orc_hash3(seed, stream * 4, e) & 15u) << (4 * i);
+        }
+        c[wi] = word;
+      }
+      uint16_t* s = (uint16_t*)w->scales;
+      uint16_t* z = (uint16_t*)w->zeros;
+#pragma omp parallel for schedule(static)
+      for (long long i = 0; i < (long long)sc; i++) {
+        s[i] = orc_f32_to_f16_bits((float)(fabs(orc_normal(seed, stream * 4 + 1, (uint64_t)i)) * sigma / 4.0), NULL);
+        z[i] = orc_f32_to_f16_bits((float)(7 + (orc_hash3(seed, stream * 4 + 2, (uint64_t)i) & 1u)), NULL);
+      }
+    } break;
+    case ORC_FORM_I4_SYM:
+      orc_synth_int4_sym(seed, stream, K, N, sigma / 4.0, (uint32_t*)w->plane, (uint16_t*)w->scales);
+      break;
+  }
+}
+
+int orc_model_synth(orc_model* m, uint64_t seed, int form, double sigma, int layers_limit) {
+  int emb_form = form == ORC_FORM_F16 ? ORC_FORM_F16 : ORC_FORM_I8;
+  synth_weight(&m->embed, seed, 1, emb_form, m->V, m->d, sigma);
+  synth_weight(&m->lm_head, seed, 3, form, m->d, m->V, sigma);
+  free(m->final_norm);
+  m->final_norm = (float*)malloc(sizeof(float) * (size_t)m->d);
+  for (int i = 0; i < m->d; i++) m->final_norm[i] = 1.0f;
+  int L = layers_limit < 0 || layers_limit > m->L ? m->L : layers_limit;
+  for (int l = 0; l < L; l++) {
+    int dims[P_NLAYER][2] = {{0, 0}, {m->d, m->H * m->dh}, {m->d, m->Hkv * m->dh},
+                             {m->d, m->Hkv * m->dh}, {m->H * m->dh, m->d}, {0, 0}, {0, 0},
+                             {0, 0}, {m->d, m->f}, {m->d, m->f}, {m->f, m->d}};
+    for (int p = 0; p < P_NLAYER; p++) {
+      uint64_t stream = (uint64_t)(l + 1) * 64 + (uint64_t)p;
+      if (p == P_ATTN_NORM || p == P_FFN_NORM || p == P_QNORM || p == P_KNORM) {
+        int w = (p == P_QNORM || p == P_KNORM) ? m->dh : m->d;
+        free(m->gains[l * P_NLAYER + p]);
+        float* g = (float*)malloc(sizeof(float) * (size_t)w);
+        for (int i = 0; i < w; i++) g[i] = 1.0f;
+        m->gains[l * P_NLAYER + p] = g;
+      } else {
+        synth_weight(&m->lw[l * P_NLAYER + p], seed, stream, form, dims[p][0], dims[p][1], sigma);
+      }
+    }
+  }
+  return 0;
+}
+
+static void cpu_linear_w(const float* x, int M, const orc_weight* w, float* y) {
+  orc_cpu_linear(x, M, w->K, w->N, w->form, w->plane, w->scales, w->zeros, y);
+}
+
+/* RMSNorm in f32 over rows of width w (nn/blocks.go:53-55). */
+static void cpu_rmsnorm(const float* x, const float* g, int rows, int w, float eps, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; r++) {
+    const float* xr = x + (size_t)r * w;
+    float s = 0;
+    for (int c = 0; c < w; c++) s += xr[c] * xr[c];
+    float sc = 1.0f / sqrtf(s / (float)w + eps);
+    for (int c = 0; c < w; c++) out[(size_t)r * w + c] = xr[c] * sc * g[c];
+  }
+}
+
+/* Interleaved RoPE in place on rows of width dh with one position per row
+ * (nn/attention.go:203-211; internal/oracle/rope.go:83-146): the angle is
+ * pos * base^(-2i/dh) evaluated in double, its sine and cosine rounded to f32,
+ * and the rotation done in f32. */
+static void cpu_rope(float* x, int rows, int dh, double base, const uint32_t* pos) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; r++) {
+    for (int i = 0; i < dh / 2; i++) {
+      double ang = (double)pos[r] * pow(base, -2.0 * (double)i / (double)dh);
+      float c = (float)cos(ang), s = (float)sin(ang);
+      float a = x[(size_t)r * dh + 2 * i], b = x[(size_t)r * dh + 2 * i + 1];
+      x[(size_t)r * dh + 2 * i] = a * c - b * s;
+      x[(size_t)r * dh + 2 * i + 1] = a * s + b * c;
+    }
+  }
+}
+
+/* One batched step in the order model/qwen3_graph.go:32-128 records it. */
+int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uint32_t* posq,
+                   const uint32_t* posk, const uint32_t* slots, const uint32_t* lengths,
+                   const uint32_t* extents, const uint32_t* last, const uint32_t* pages,
+                   int max_pages, float* logits, int layers) {
+  int T = rows, d = m->d, H = m->H, Hkv = m->Hkv, dh = m->dh, f = m->f, V = m->V;
+  int qw = H * dh, kw = Hkv * dh;
+  int L = layers < 0 || layers > m->L ? m->L : layers;
+  float* h = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* n = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* q = (float*)malloc(sizeof(float) * (size_t)T * qw);
+  float* k = (float*)malloc(sizeof(float) * (size_t)T * kw);
+  float* v = (float*)malloc(sizeof(float) * (size_t)T * kw);
+  float* a = (float*)malloc(sizeof(float) * (size_t)T * qw);
+  float* y = (float*)malloc(sizeof(float) * (size_t)T * (d > f ? d : f));
+  float* gt = (float*)malloc(sizeof(float) * (size_t)T * f);
+  float* up = (float*)malloc(sizeof(float) * (size_t)T * f);
+  /* rows 3: embedding (model/qwen3_graph.go:54-61) */
+  {
+    float* row = (float*)malloc(sizeof(float) * (size_t)d);
+    for (int t = 0; t < T; t++) {
+      deq_row(m->embed.form, m->embed.plane, m->embed.scales, m->embed.zeros, V, d, (int)ids[t], row);
+      memcpy(h + (size_t)t * d, row, sizeof(float) * (size_t)d);
+    }
+    free(row);
+  }
+  float scale = (float)(1.0 / sqrt((double)dh)); /* session.go:821-823 */
+  size_t layer_kv = (size_t)m->C * Hkv * dh;
+  for (int l = 0; l < L; l++) {
+    orc_weight* W = m->lw + (size_t)l * P_NLAYER;
+    float** G = m->gains + (size_t)l * P_NLAYER;
+    cpu_rmsnorm(h, G[P_ATTN_NORM], T, d, m->eps, n);
+    cpu_linear_w(n, T, &W[P_WQ], q);
+    cpu_linear_w(n, T, &W[P_WK], k);
+    cpu_linear_w(n, T, &W[P_WV], v);
+    cpu_rmsnorm(q, G[P_QNORM], T * H, dh, m->eps, q);
+    cpu_rmsnorm(k, G[P_KNORM], T * Hkv, dh, m->eps, k);
+    cpu_rope(q, T * H, dh, (double)m->theta, posq);
+    cpu_rope(k, T * Hkv, dh, (double)m->theta, posk);
+    /* Cast + ScatterRows, slot >= C dropped (nn/attention.go:225-232; plan.go:182-192) */
+    uint16_t* kl = m->kc + (size_t)l * layer_kv;
+    uint16_t* vl = m->vc + (size_t)l * layer_kv;
+    for (int t = 0; t < T; t++) {
+      if ((int)slots[t] >= m->C) continue;
+      for (int i = 0; i < kw; i++) {
+        kl[(size_t)slots[t] * kw + i] = orc_f32_to_f16_ieee(k[(size_t)t * kw + i]);
+        vl[(size_t)slots[t] * kw + i] = orc_f32_to_f16_ieee(v[(size_t)t * kw + i]);
+      }
+    }
+    orc_cpu_ragged_attention(q, T, H, Hkv, dh, kl, vl, B, lengths, extents, pages, max_pages,
+                             m->block, scale, a);
+    cpu_linear_w(a, T, &W[P_WO], y);
+    for (size_t i = 0; i < (size_t)T * d; i++) h[i] += y[i];
+    cpu_rmsnorm(h, G[P_FFN_NORM], T, d, m->eps, n);
+    cpu_linear_w(n, T, &W[P_WGATE], gt);
+    cpu_linear_w(n, T, &W[P_WUP], up);
+    for (size_t i = 0; i < (size_t)T * f; i++) gt[i] = gt[i] / (1.0f + expf(-gt[i])) * up[i];
+    cpu_linear_w(gt, T, &W[P_WDOWN], y);
+    for (size_t i = 0; i < (size_t)T * d; i++) h[i] += y[i];
+  }
+  /* rows 26-28: last row per sequence, final norm, head (model/qwen3_graph.go:117-127) */
+  float* lastrows = (float*)malloc(sizeof(float) * (size_t)B * d);
+  for (int s = 0; s < B; s++) memcpy(lastrows + (size_t)s * d, h + (size_t)last[s] * d, sizeof(float) * (size_t)d);
+  cpu_rmsnorm(lastrows, m->final_norm, B, d, m->eps, lastrows);
+  cpu_linear_w(lastrows, B, &m->lm_head, logits);
+  for (int s = 0; s < B; s++)
+    if (extents[s] == 0) memset(logits + (size_t)s * V, 0, sizeof(float) * (size_t)V);
+  free(lastrows);
+  free(h); free(n); free(q); free(k); free(v); free(a); free(y); free(gt); free(up);
+  return 0;
+}

@@ -1,0 +1,154 @@
+"""nn.Linear on the GPU (every weight form) against the CPU restatement.
+
+Dequantization is bit-exact: the device's f32 dequant equals the host
+restatement's, and the f16 operand the MFMA multiplies equals the
+round-to-nearest-even f16 of that value. The product is compared with a
+float64 matmul of exactly those operands, so the only budget is f32
+accumulation, written here as in tolerance.go:
+    |y - y_ref| <= 4 * sqrt(K) * 2^-24 * sum_k |x_k w_k|      (AccumF32(K), headroom 4)
+plus, when the activation is f32 and carried as f16 hi + lo, the low part's
+own rounding: 2^-22 * sum |x_k w_k|.
+Against the unrounded f32 weights (tgo's CPU path) the budget adds the f16
+operand term StoreF16: 2^-11 per rounded operand.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+FORMS = {0: "f16", 1: "int8", 2: "int4-tgo", 3: "int4-sym"}
+
+
+def make_weight(form, K, N, rng):
+    w = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    if form == 0:
+        return dict(plane=oracle.f16_bits(w)), None
+    if form == 1:
+        q = np.empty(K * N, np.int8)
+        s = np.empty((K * N + 31) // 32, np.uint16)
+        oracle.lib.orc_quantize_int8(oracle.ptr(w.ravel().copy()), K * N, oracle.ptr(q), oracle.ptr(s))
+        return dict(plane=q, scales=s), None
+    if form == 2:
+        c = np.empty((K * N + 7) // 8, np.uint32)
+        s = np.empty((K * N + 127) // 128, np.uint16)
+        z = np.empty((K * N + 127) // 128, np.uint16)
+        oracle.lib.orc_quantize_int4_tgo(oracle.ptr(w.ravel().copy()), K * N, oracle.ptr(c),
+                                         oracle.ptr(s), oracle.ptr(z))
+        return dict(plane=c, scales=s, zeros=z), None
+    qw, sc = oracle.synth_int4_sym(7, 3, K, N, 0.01)
+    return dict(plane=qw, scales=sc), None
+
+
+def deq(form, K, N, wd):
+    return oracle.dequant(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+
+
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+def test_dequant_is_bit_exact(ctx, torch_gpu, form):
+    torch = torch_gpu
+    rng = np.random.default_rng(form)
+    K, N = 256, 384
+    wd, _ = make_weight(form, K, N, rng)
+    h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    try:
+        y = torch.empty((K, N), dtype=torch.float32, device="cuda")
+        ctx.dequant(h, y)
+        y16 = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        ctx.dequant_f16(h, y16)
+        torch.cuda.synchronize()
+        want = deq(form, K, N, wd)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(y16.cpu().numpy().view(np.uint16),
+                              want.astype(np.float16).view(np.uint16))
+    finally:
+        ctx.weight_free(h)
+
+
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [1, 8, 33, 64, 130, 300])
+@pytest.mark.parametrize("xf32", [True, False])
+def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xf32):
+    torch = torch_gpu
+    import tgo_amd
+    rng = np.random.default_rng(100 + form * 7 + M)
+    K, N = 512, 256 if form != 2 else 384
+    wd, _ = make_weight(form, K, N, rng)
+    w32 = deq(form, K, N, wd)
+    w16 = w32.astype(np.float16).astype(np.float64)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    try:
+        if xf32:
+            dx = torch.from_numpy(x).cuda()
+            xu = x.astype(np.float64)
+        else:
+            dx = torch.from_numpy(x.astype(np.float16)).cuda()
+            xu = x.astype(np.float16).astype(np.float64)
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.linear(h, dx, M, y, x_dtype=tgo_amd.F32 if xf32 else tgo_amd.F16)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().astype(np.float64)
+    finally:
+        ctx.weight_free(h)
+    ref = xu @ w16
+    mag = np.abs(xu) @ np.abs(w16)
+    tol = (4 * np.sqrt(K) * 2.0 ** -24 + (2.0 ** -22 if xf32 else 0)) * mag + 1e-30
+    assert np.all(np.abs(got - ref) <= tol), np.max(np.abs(got - ref) / tol)
+    # against tgo's CPU path (f32 activations, unrounded f32 weights)
+    cpu = oracle.cpu_linear(x, form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    mag2 = np.abs(x.astype(np.float64)) @ np.abs(w32.astype(np.float64))
+    tol2 = (2.0 ** -11 * (1 if xf32 else 2) + 8 * np.sqrt(K) * 2.0 ** -24) * mag2
+    assert np.all(np.abs(got - cpu) <= tol2)
+
+
+def test_linear_is_deterministic_and_row_independent(ctx, torch_gpu):
+    """A row's result does not depend on the rows beside it when the tile
+    configuration is the same (M in one tile class)."""
+    torch = torch_gpu
+    import tgo_amd
+    rng = np.random.default_rng(3)
+    K, N = 1024, 512
+    qw, sc = oracle.synth_int4_sym(1, 9, K, N, 0.01)
+    h = ctx.weight_upload(3, K, N, qw, sc)
+    try:
+        x = torch.randn(200, K, device="cuda").half()
+        y1 = torch.empty(200, N, device="cuda")
+        y2 = torch.empty(200, N, device="cuda")
+        ctx.linear(h, x, 200, y1, x_dtype=tgo_amd.F16)
+        ctx.linear(h, x, 200, y2, x_dtype=tgo_amd.F16)
+        x2 = x.clone()
+        x2[150:] = 0
+        y3 = torch.empty(200, N, device="cuda")
+        ctx.linear(h, x2, 200, y3, x_dtype=tgo_amd.F16)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
+        assert torch.equal(y1[:128], y3[:128])
+    finally:
+        ctx.weight_free(h)
+
+
+@pytest.mark.parametrize("KN", [(4096, 12288), (12288, 4096), (4096, 6144)])
+def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
+    """BASELINE config 3 shapes (int4 symmetric, group 32 along K) at M = 1..1024,
+    checked on sampled columns against the f64 product of the same operands."""
+    torch = torch_gpu
+    import tgo_amd
+    K, N = KN
+    h = ctx.weight_synth(3, K, N, 42, 5, 0.02)
+    try:
+        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        ctx.dequant_f16(h, wf)
+        for M in (1, 8, 64, 256, 1024):
+            x = torch.randn(M, K, device="cuda").half()
+            y = torch.empty(M, N, device="cuda")
+            ctx.linear(h, x, M, y, x_dtype=tgo_amd.F16)
+            torch.cuda.synchronize()
+            cols = torch.arange(0, N, N // 64, device="cuda")
+            ref = x.double() @ wf[:, cols].double()
+            mag = x.double().abs() @ wf[:, cols].double().abs()
+            tol = 4 * (K ** 0.5) * 2.0 ** -24 * mag
+            assert bool(((y[:, cols].double() - ref).abs() <= tol).all()), M
+    finally:
+        ctx.weight_free(h)

@@ -1,0 +1,143 @@
+// common.h -- shared definitions for libtgohip (HIP/CDNA4, gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+#include <vector>
+
+#include "../../include/tgohip.h"
+
+namespace tgohip {
+
+// Thread-local last error; every entry point that fails sets it.
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+std::string hip_message(hipError_t e, const char* what);
+
+#define TGOHIP_HIP(call)                                                    \
+  do {                                                                      \
+    hipError_t _e = (call);                                                 \
+    if (_e != hipSuccess) return ::tgohip::fail(TGOHIP_EDEVICE, ::tgohip::hip_message(_e, #call)); \
+  } while (0)
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// ---- attention plan (built on the host from lengths/extents) ----------
+// One work item: a (sequence, kv head) pair's rows [tok0, tok0+ntok) of the
+// sequence's extent against positions [kv_lo, kv_hi).
+struct AttnItem {
+  int32_t seq;
+  int32_t kvh;
+  int32_t tok0;
+  int32_t ntok;
+  int32_t kv_lo;
+  int32_t kv_hi;
+  int32_t part;  // partial slot for a split item, -1 when the item writes `out`
+  int32_t mode;  // 0: rows <= 16, the four waves split the positions; 1: waves split rows
+};
+// One combine item: merges nparts partial results of a (sequence, kv head, tokens).
+struct AttnCombine {
+  int32_t seq;
+  int32_t kvh;
+  int32_t tok0;
+  int32_t ntok;
+  int32_t part0;
+  int32_t nparts;
+  int32_t pad0, pad1;
+};
+
+constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
+constexpr int kAttnSplit = 512;   // positions per split of a decode-style item
+constexpr int kAttnRowsP = 128;   // rows per prefill-style item (4 waves x 32)
+constexpr int kHeadDim = 128;
+
+struct AttnPlan {
+  std::vector<AttnItem> items;
+  std::vector<AttnCombine> combines;
+  std::vector<int32_t> cu;  // [B] flat row offset of each sequence
+  int parts = 0;
+  int claimed = 0;          // sum of extents
+};
+
+
+// ---- GEMM (kernels/gemm.hip) --------------------------------------------
+enum { EPI_F32 = 0, EPI_F16 = 1, EPI_RESID = 2, EPI_SWIGLU_F16 = 3, EPI_SWIGLU_F32 = 4 };
+
+// A weight in the fragment-major device layout (see kernels/gemm.hip).
+struct PackedWeight {
+  int form = -1, K = 0, N = 0;
+  void* wp = nullptr;
+  half_t* ws = nullptr;
+  half_t* wz = nullptr;
+};
+
+size_t packed_payload_bytes(int form, int K, int N);
+size_t packed_scale_halves(int form, int K, int N);
+// Repacks a canonical weight (device memory) into w. The sub-weight's n-block
+// nb lands at n-block nb*nb_stride + nb_off of w (fused QKV / gate-up).
+int repack_enqueue(int form, const void* plane, const uint16_t* scales, const uint16_t* zeros,
+                   int K, int N, PackedWeight& w, int nb_stride, int nb_off, hipStream_t st);
+int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t st);
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu);
+int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
+                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st);
+
+// ---- attention (kernels/attention.hip) -----------------------------------
+struct AttnDevPlan {
+  const AttnItem* items;
+  const AttnCombine* combines;
+  const int32_t* cu;
+  const uint32_t* lengths;
+  const uint32_t* extents;
+  const uint32_t* pages;
+  float* part_o;
+  float* part_ml;
+};
+int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
+                    const uint32_t* pages, int max_pages, int block, int capacity, int H,
+                    int Hkv, AttnPlan& plan);
+int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int q_f16,
+                 const void* k, const void* v, void* out, int out_f16, int T, int H, int Hkv,
+                 int max_pages, int block, float scale, hipStream_t stream);
+
+// ---- per-row kernels (kernels/elementwise.hip) ---------------------------
+struct QKRopeArgs {
+  const float* qkv;       // [T, (H + 2*Hkv) * 128]
+  const float* qnorm;     // [128]
+  const float* knorm;     // [128]
+  const uint32_t* posq;   // [T*H]
+  const uint32_t* posk;   // [T*Hkv]
+  const uint32_t* slots;  // [T]
+  const double* inv_freq; // [64]: base^(-2i/128), computed once on the host in double
+  float* q;               // [T, H, 128]
+  half_t* kc;             // layer view [C, Hkv, 128]
+  half_t* vc;
+  int H, Hkv, capacity;
+  float eps;
+};
+void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
+                  int d, float* h, hipStream_t st);
+void launch_rmsnorm(const float* x, const uint32_t* rows, int nrows, const float* g, int w,
+                    float eps, void* out, int out_f16, hipStream_t st);
+void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st);
+void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
+                   hipStream_t st);
+void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st);
+void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
+                      hipStream_t st);
+void launch_synth_absf16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
+                         hipStream_t st);
+void launch_synth_i4sym(uint64_t seed, uint64_t stream, int K, int N, uint32_t* out, hipStream_t st);
+void launch_synth_i4tgo(uint64_t seed, uint64_t stream, size_t n, uint32_t* out, hipStream_t st);
+void launch_synth_zero(uint64_t seed, uint64_t stream, size_t n, uint16_t* out, hipStream_t st);
+void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipStream_t st);
+void launch_fill_f32(float* p, size_t n, float v, hipStream_t st);
+
+}  // namespace tgohip

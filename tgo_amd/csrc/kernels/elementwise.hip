@@ -1,0 +1,309 @@
+// elementwise.hip -- the per-row kernels around the projections and attention
+// of one step (model/qwen3_graph.go:32-128):
+//   embed_kernel        GatherRows / QuantGatherRows of the embedding (:54-61)
+//   rmsnorm_kernel      RMSNorm (nn/blocks.go:53-55) fused with the cast to the
+//                       next projection's operand dtype, optionally gathering
+//                       rows (the head's GatherRows(h, last), :117)
+//   qk_rope_kv_kernel   q/k RMSNorm per head + interleaved RoPE + f16 narrowing +
+//                       ScatterRows into the paged pool, slot >= capacity dropped
+//                       (nn/attention.go:192-232, plan.go:182-192)
+//   argmax_kernel       greedy token, first strict maximum (sample/stages.go:196)
+//   synth_* kernels     seeded random-init weights, bit-identical to the CPU
+//                       restatement's generator
+#include "../common.h"
+
+namespace tgohip {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// h[t, :] = table[ids[t], :] (f16) or q * scale (int8, one scale per 32
+// flattened elements).
+__global__ void embed_kernel(const uint32_t* ids, const void* table, const uint16_t* scales,
+                             int form, int d, float* h) {
+  const int t = blockIdx.x;
+  const size_t base = (size_t)ids[t] * d;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    float v;
+    if (form == TGOHIP_FORM_F16) {
+      v = (float)((const half_t*)table)[base + i];
+    } else {
+      const size_t e = base + i;
+      v = (float)((const int8_t*)table)[e] * (float)(*(const half_t*)&scales[e / 32]);
+    }
+    h[(size_t)t * d + i] = v;
+  }
+}
+
+// out[r, :] = x[src(r), :] * rsqrt(mean(x^2) + eps) * g, stored f16 or f32.
+// src(r) = rows ? rows[r] : r. One 256-thread block per row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint32_t* rows,
+                                                      const float* g, int w, float eps,
+                                                      void* out, int out_f16) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const size_t src = (size_t)(rows ? rows[r] : (uint32_t)r) * w;
+  float ss = 0.f;
+  for (int i = threadIdx.x * 4; i < w; i += 1024) {
+    const float4_t v = *(const float4_t*)(x + src + i);
+    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  }
+  ss = block_sum256(ss, red);
+  const float sc = 1.0f / sqrtf(ss / (float)w + eps);
+  for (int i = threadIdx.x * 4; i < w; i += 1024) {
+    const float4_t v = *(const float4_t*)(x + src + i);
+    const float4_t gg = *(const float4_t*)(g + i);
+    float4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = v[j] * sc * gg[j];
+    if (out_f16) {
+      half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+      *(half4_t*)((half_t*)out + (size_t)r * w + i) = hv;
+    } else {
+      *(float4_t*)((float*)out + (size_t)r * w + i) = o;
+    }
+  }
+}
+
+
+// One block (4 waves) per token; a wave takes one head row at a time and a
+// lane owns the rotated pair (2*lane, 2*lane+1).
+__global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int W = (a.H + 2 * a.Hkv) * kHeadDim;
+  const float* row = a.qkv + (size_t)t * W;
+  const uint32_t slot = a.slots[t];
+  const bool write = slot < (uint32_t)a.capacity;
+  int cpos = -1;
+  float c = 1.f, s = 0.f;
+  const double inv = a.inv_freq[lane];
+  for (int hh = wave; hh < a.H + 2 * a.Hkv; hh += 4) {
+    const float2 v = *(const float2*)(row + hh * kHeadDim + 2 * lane);
+    if (hh >= a.H + a.Hkv) {
+      // value head: narrowed and scattered as is
+      if (write) {
+        const int vh = hh - a.H - a.Hkv;
+        half2_t hv = {(half_t)v.x, (half_t)v.y};
+        *(half2_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHeadDim + 2 * lane) = hv;
+      }
+      continue;
+    }
+    const bool isq = hh < a.H;
+    const float* gain = isq ? a.qnorm : a.knorm;
+    const float ss = wave_sum(v.x * v.x + v.y * v.y);
+    const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
+    const float x0 = v.x * sc * gain[2 * lane], x1 = v.y * sc * gain[2 * lane + 1];
+    const int pos = isq ? (int)a.posq[(size_t)t * a.H + hh] : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
+    if (pos != cpos) {
+      const double ang = (double)pos * inv;
+      c = (float)cos(ang);
+      s = (float)sin(ang);
+      cpos = pos;
+    }
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    if (isq) {
+      *(float2*)(a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = make_float2(y0, y1);
+    } else if (write) {
+      const int kh = hh - a.H;
+      half2_t hk = {(half_t)y0, (half_t)y1};
+      *(half2_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHeadDim + 2 * lane) = hk;
+    }
+  }
+}
+
+// First index of the strict maximum of each row (sample/stages.go:196-206).
+__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int V,
+                                                     const uint32_t* extents, int32_t* out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int b = blockIdx.x;
+  const float* row = logits + (size_t)b * V;
+  float best = -INFINITY;
+  int bi = -1;
+  for (int i = threadIdx.x; i < V; i += 256) {
+    const float v = row[i];
+    if (bi < 0 || v > best) { best = v; bi = i; }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const float v2 = sv[threadIdx.x + o];
+      const int i2 = si[threadIdx.x + o];
+      const float v1 = sv[threadIdx.x];
+      const int i1 = si[threadIdx.x];
+      if (i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1))) {
+        sv[threadIdx.x] = v2;
+        si[threadIdx.x] = i2;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[b] = extents[b] == 0 ? -1 : si[0];
+}
+
+// Zeroes the logits rows of members that contributed nothing.
+__global__ void zero_idle_rows_kernel(float* logits, int V, const uint32_t* extents) {
+  const int b = blockIdx.x;
+  if (extents[b] != 0) return;
+  for (int i = threadIdx.x; i < V; i += blockDim.x) logits[(size_t)b * V + i] = 0.f;
+}
+
+// ---- seeded synthesis (the CPU restatement's generator, restated) ---------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t hash3(uint64_t seed, uint64_t stream, uint64_t idx) {
+  return splitmix64(splitmix64(seed * 0x100000001B3ull + stream) + idx);
+}
+__device__ __forceinline__ double normal_ih(uint64_t seed, uint64_t stream, uint64_t idx) {
+  const uint64_t m = (1ull << 21) - 1;
+  int64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint64_t h = hash3(seed, stream, idx * 4 + (uint64_t)j);
+    s += (int64_t)(h & m) + (int64_t)((h >> 21) & m) + (int64_t)((h >> 42) & m);
+  }
+  return (double)(s - 6 * (int64_t)(1 << 21)) / (double)(1 << 21);
+}
+
+// f32ToF16Bits (weights/convert.go:153-180) on the device: NaN -> 0x7e00,
+// saturate to +-65504, flush below 2^-14 keeping sign, else RNE.
+__device__ __forceinline__ uint16_t f16_loader_bits(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7e00;
+  const float a = __uint_as_float(b & 0x7fffffffu);
+  if (a > 65504.0f) return sign | 0x7bff;
+  if (a < 1.0f / 16384.0f) return sign;
+  const int32_t e = (int32_t)((b >> 23) & 0xff) - 127;
+  const uint32_t mant = b & 0x7fffffu;
+  uint32_t keep = mant >> 13;
+  const uint32_t rest = mant & 0x1fffu, half = 0x1000u;
+  if (rest > half || (rest == half && (keep & 1))) keep++;
+  return (uint16_t)(sign | (uint16_t)(((uint32_t)(e + 15) << 10) + keep));
+}
+
+// F16 plane: loader-rule f16 of f32(N(0,1) * sigma).
+__global__ void synth_f16_kernel(uint64_t seed, uint64_t stream, size_t n, double sigma,
+                                 uint16_t* out) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = f16_loader_bits((float)(normal_ih(seed, stream, i) * sigma));
+}
+// |N(0,1)| * sigma as loader-rule f16 (scales).
+__global__ void synth_absf16_kernel(uint64_t seed, uint64_t stream, size_t n, double sigma,
+                                    uint16_t* out) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = f16_loader_bits((float)(fabs(normal_ih(seed, stream, i)) * sigma));
+}
+// I4_SYM codes: word (r, n) of [K/8][N], k = 8r+i -> nibble hash&15.
+__global__ void synth_i4sym_kernel(uint64_t seed, uint64_t stream, int K, int N, uint32_t* out) {
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)(K / 8) * N) return;
+  const size_t r = t / N, n = t % N;
+  uint32_t w = 0;
+  for (int i = 0; i < 8; i++) {
+    const uint64_t e = (uint64_t)(r * 8 + i) * (uint64_t)N + n;
+    w |= (uint32_t)(hash3(seed, stream, e) & 15u) << (4 * i);
+  }
+  out[t] = w;
+}
+// I4_TGO codes over the flattened plane: element e -> hash&15.
+__global__ void synth_i4tgo_kernel(uint64_t seed, uint64_t stream, size_t n, uint32_t* out) {
+  const size_t wi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (wi >= (n + 7) / 8) return;
+  uint32_t w = 0;
+  for (int i = 0; i < 8; i++) {
+    const size_t e = wi * 8 + i;
+    if (e < n) w |= (uint32_t)(hash3(seed, stream, e) & 15u) << (4 * i);
+  }
+  out[wi] = w;
+}
+// I4_TGO zeros: 7 + (hash & 1) as f16.
+__global__ void synth_zero_kernel(uint64_t seed, uint64_t stream, size_t n, uint16_t* out) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = f16_loader_bits((float)(7 + (hash3(seed, stream, i) & 1u)));
+}
+// I8 codes: hash % 255 - 127.
+__global__ void synth_i8_kernel(uint64_t seed, uint64_t stream, size_t n, int8_t* out) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (int8_t)((int)(hash3(seed, stream, i) % 255u) - 127);
+}
+__global__ void fill_f32_kernel(float* p, size_t n, float v) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+__global__ void zero_u32_kernel(uint32_t* p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// ---- host launchers --------------------------------------------------------
+static inline dim3 grid1(size_t n, int b = 256) { return dim3((unsigned)((n + b - 1) / b)); }
+
+void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
+                  int d, float* h, hipStream_t st) {
+  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, st, ids, table, scales, form, d, h);
+}
+void launch_rmsnorm(const float* x, const uint32_t* rows, int nrows, const float* g, int w,
+                    float eps, void* out, int out_f16, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, st, x, rows, g, w, eps, out, out_f16);
+}
+void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
+  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);
+}
+void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
+                   hipStream_t st) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, st, logits, V, extents, out);
+}
+void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st) {
+  hipLaunchKernelGGL(zero_idle_rows_kernel, dim3(B), dim3(256), 0, st, logits, V, extents);
+}
+void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
+                      hipStream_t st) {
+  hipLaunchKernelGGL(synth_f16_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, sigma, out);
+}
+void launch_synth_absf16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
+                         hipStream_t st) {
+  hipLaunchKernelGGL(synth_absf16_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, sigma, out);
+}
+void launch_synth_i4sym(uint64_t seed, uint64_t stream, int K, int N, uint32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(synth_i4sym_kernel, grid1((size_t)(K / 8) * N), dim3(256), 0, st, seed, stream, K, N, out);
+}
+void launch_synth_i4tgo(uint64_t seed, uint64_t stream, size_t n, uint32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(synth_i4tgo_kernel, grid1((n + 7) / 8), dim3(256), 0, st, seed, stream, n, out);
+}
+void launch_synth_zero(uint64_t seed, uint64_t stream, size_t n, uint16_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(synth_zero_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, out);
+}
+void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(synth_i8_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, out);
+}
+void launch_fill_f32(float* p, size_t n, float v, hipStream_t st) {
+  hipLaunchKernelGGL(fill_f32_kernel, grid1(n), dim3(256), 0, st, p, n, v);
+}
+void launch_zero_u32(uint32_t* p, size_t n, hipStream_t st) {
+  hipLaunchKernelGGL(zero_u32_kernel, grid1(n), dim3(256), 0, st, p, n);
+}
+
+}  // namespace tgohip

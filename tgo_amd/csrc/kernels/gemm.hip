@@ -1,0 +1,618 @@
+// gemm.hip -- nn.Linear (nn/blocks.go:22-46): y[M,N] = x[M,K] . deq(W)[K,N] with
+// the dequantization fused into the MFMA B operand, for every weight form tgo
+// stores (nn/nn.go:118-136) plus the symmetric group-32-along-K int4 pack.
+//
+// Device weight layout ("fragment-major"), built once at upload by
+// repack_kernel: for each block of 32 output columns (nb) and each 64-deep
+// slice of K (ks), lane l of a wave owns column nb*32 + l%32 and, for substep
+// j = 0..3, the eight k = ks*64 + 16j + 8*(l/32) + [0,8) -- exactly the B
+// fragment of v_mfma_f32_32x32x16_f16. A wave therefore reads its weights with
+// one contiguous 1 KiB (int4) / 2 KiB (int8) / 4 KiB (f16) burst per (nb, ks),
+// dequantizes in registers and never stages weights through LDS.
+//   int4: one u32 per substep; nibble slots hold k offsets 0,2,4,6,1,3,5,7 so
+//         ((w >> 4j) & 0x000F000F) | 0x64006400 is the f16 pair (1024+q_2j,
+//         1024+q_2j+1).
+//   int8: two u32 per substep; bytes hold k offsets 0,2,1,3 as q+128 so the
+//         0x00FF00FF mask yields consecutive-k f16 pairs (1024+b).
+//   f16:  eight halves per substep.
+// Dequantized value: round-to-nearest-even f16 of the exact (q - z) * s, which
+// is computed with one exact packed subtraction and one rounded packed multiply.
+//
+// Tiling: 256 threads = 4 waves side by side in N; a workgroup owns MW rows x
+// 256 columns; each wave MW x 64 (MW/32 x 2 MFMA blocks of 32x32). The
+// activation tile (MW x 64 f16) is double-buffered in LDS, XOR-swizzled. An f32
+// activation is carried as f16 hi + lo (two MFMAs) so the product keeps ~22
+// bits of the activation. Split-K over grid.z writes f32 partials that a
+// reduction kernel sums in split order (deterministic) and finishes.
+#include "../common.h"
+
+#include <algorithm>
+
+namespace tgohip {
+
+struct GemmArgs {
+  const void* x;        // [M,K] f16 or f32
+  const void* wp;       // packed payload
+  const half_t* ws;     // packed scales (form dependent)
+  const half_t* wz;     // packed zero+1024 (I4_TGO only)
+  void* y;              // output (EPI dependent)
+  float* part;          // split-K partials [splits][M][N]
+  int M, K, N;
+  int ksteps_per_split;
+};
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) {
+  union { uint32_t u; half2_t h; } c;
+  c.u = u;
+  return c.h;
+}
+
+// ---- dequantization of one substep's B fragment (8 consecutive k) ----------
+__device__ __forceinline__ half8_t deq_i4_sym(uint32_t w, half_t s) {
+  const half2_t sp = {s, s};
+  const half2_t bias = {(half_t)1032.f, (half_t)1032.f};
+  half8_t o;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    half2_t h = as_h2(((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u);
+    h = h - bias;
+    h = h * sp;
+    o[2 * j] = h[0];
+    o[2 * j + 1] = h[1];
+  }
+  return o;
+}
+__device__ __forceinline__ half8_t deq_i4_asym(uint32_t w, half8_t s, half8_t zz) {
+  half8_t o;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    half2_t h = as_h2(((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u);
+    const half2_t z2 = {zz[2 * j], zz[2 * j + 1]};
+    const half2_t s2 = {s[2 * j], s[2 * j + 1]};
+    h = h - z2;
+    h = h * s2;
+    o[2 * j] = h[0];
+    o[2 * j + 1] = h[1];
+  }
+  return o;
+}
+__device__ __forceinline__ half8_t deq_i8(uint32_t w0, uint32_t w1, half8_t s) {
+  const half2_t bias = {(half_t)1152.f, (half_t)1152.f};
+  half8_t o;
+  const uint32_t ws[2] = {w0, w1};
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    half2_t lo = as_h2((ws[u] & 0x00FF00FFu) | 0x64006400u);
+    half2_t hi = as_h2(((ws[u] >> 8) & 0x00FF00FFu) | 0x64006400u);
+    const half2_t s0 = {s[4 * u], s[4 * u + 1]}, s1 = {s[4 * u + 2], s[4 * u + 3]};
+    lo = (lo - bias) * s0;
+    hi = (hi - bias) * s1;
+    o[4 * u] = lo[0];
+    o[4 * u + 1] = lo[1];
+    o[4 * u + 2] = hi[0];
+    o[4 * u + 3] = hi[1];
+  }
+  return o;
+}
+
+// Per-form payload sizes (bytes per lane per (nb, ks)).
+template <int FORM> struct Payload;
+template <> struct Payload<TGOHIP_FORM_F16> { static constexpr int bytes = 64; };
+template <> struct Payload<TGOHIP_FORM_I8> { static constexpr int bytes = 32; };
+template <> struct Payload<TGOHIP_FORM_I4_TGO> { static constexpr int bytes = 16; };
+template <> struct Payload<TGOHIP_FORM_I4_SYM> { static constexpr int bytes = 16; };
+
+// The lane's raw material for one (nb, ks): payload plus scales.
+template <int FORM>
+struct BRaw {
+  uint4 p[Payload<FORM>::bytes / 16];
+  uint4 s[4];   // per-k scales (I8, I4_TGO): 8 halves per substep; I4_SYM uses s[0].x
+  uint4 z[4];   // per-k zero+1024 (I4_TGO)
+};
+
+template <int FORM>
+__device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
+                                          BRaw<FORM>& r) {
+  const int KS = g.K / 64;
+  const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
+  const uint4* pp = (const uint4*)((const char*)g.wp + slot * Payload<FORM>::bytes);
+#pragma unroll
+  for (int i = 0; i < Payload<FORM>::bytes / 16; i++) r.p[i] = pp[i];
+  if (FORM == TGOHIP_FORM_I4_SYM) {
+    const uint32_t* sp = (const uint32_t*)(g.ws) + ((size_t)nb * KS + ks) * 32 + (lane & 31);
+    r.s[0].x = *sp;
+  } else if (FORM == TGOHIP_FORM_I8 || FORM == TGOHIP_FORM_I4_TGO) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const size_t o = ((((size_t)nb * KS + ks) * 4 + j) * 2 + h) * 8;
+      r.s[j] = *(const uint4*)(g.ws + o);
+      if (FORM == TGOHIP_FORM_I4_TGO) r.z[j] = *(const uint4*)(g.wz + o);
+    }
+  }
+}
+
+template <int FORM>
+__device__ __forceinline__ half8_t bfrag(const BRaw<FORM>& r, int j) {
+  union U { uint4 u; half8_t h; };
+  if (FORM == TGOHIP_FORM_F16) {
+    U c;
+    c.u = r.p[j];
+    return c.h;
+  } else if (FORM == TGOHIP_FORM_I4_SYM) {
+    const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
+    union { uint32_t u; half2_t h; } sc;
+    sc.u = r.s[0].x;
+    return deq_i4_sym(w, j < 2 ? sc.h[0] : sc.h[1]);
+  } else if (FORM == TGOHIP_FORM_I4_TGO) {
+    const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
+    U s, z;
+    s.u = r.s[j];
+    z.u = r.z[j];
+    return deq_i4_asym(w, s.h, z.h);
+  } else {
+    const uint4 q = r.p[j >> 1];
+    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
+    U s;
+    s.u = r.s[j];
+    return deq_i8(w0, w1, s.h);
+  }
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+
+template <int FORM, int MW, bool ASPLIT, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int MB = MW / 32;
+  constexpr int APLANES = ASPLIT ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) half_t As[2][APLANES][MW * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c32 = lane & 31;
+  const int NBT = g.N / 32;
+  const int nbw0 = blockIdx.x * 8 + wave * 2;
+  const int m0 = blockIdx.y * MW;
+  const int KS = g.K / 64;
+  const int ks0 = blockIdx.z * g.ksteps_per_split;
+  const int ks1 = min(KS, ks0 + g.ksteps_per_split);
+  const bool nbv[2] = {nbw0 < NBT, nbw0 + 1 < NBT};
+
+  // A tile loader: MW rows x 64 k. Each thread moves (MW*64)/256 = MW/4
+  // elements as chunks of 8.
+  constexpr int ACH = MW / 32;  // chunks of 8 elements per thread
+  uint4 areg[ACH][APLANES];
+  auto load_a = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < ACH; i++) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      const int gm = m0 + row;
+      if (gm < g.M) {
+        const size_t off = (size_t)gm * g.K + ks * 64 + kc * 8;
+        if (ASPLIT) {
+          const float4_t u = *(const float4_t*)((const float*)g.x + off);
+          const float4_t w = *(const float4_t*)((const float*)g.x + off + 4);
+          const float v[8] = {u[0], u[1], u[2], u[3], w[0], w[1], w[2], w[3]};
+          union { uint4 u; half8_t h; } hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const half_t hv = (half_t)v[e];
+            hi.h[e] = hv;
+            lo.h[e] = (half_t)(v[e] - (float)hv);
+          }
+          areg[i][0] = hi.u;
+          if (APLANES > 1) areg[i][APLANES - 1] = lo.u;
+        } else {
+          areg[i][0] = *(const uint4*)((const half_t*)g.x + off);
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < APLANES; p++) areg[i][p] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; i++) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      const int phys = row * 8 + (kc ^ (row & 7));
+#pragma unroll
+      for (int p = 0; p < APLANES; p++) ((uint4*)As[buf][p])[phys] = areg[i][p];
+    }
+  };
+
+  float16_t acc[MB][2];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
+
+  BRaw<FORM> bcur[2], bnext[2];
+  if (ks0 < ks1) {
+    load_a(ks0);
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+      if (nbv[b]) load_braw<FORM>(g, nbw0 + b, ks0, lane, bcur[b]);
+    store_a(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int ks = ks0; ks < ks1; ks++) {
+    const bool more = ks + 1 < ks1;
+    if (more) {
+      load_a(ks + 1);
+#pragma unroll
+      for (int b = 0; b < 2; b++)
+        if (nbv[b]) load_braw<FORM>(g, nbw0 + b, ks + 1, lane, bnext[b]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      half8_t bf[2];
+#pragma unroll
+      for (int b = 0; b < 2; b++) bf[b] = bfrag<FORM>(bcur[b], j);
+#pragma unroll
+      for (int mb = 0; mb < MB; mb++) {
+        const int row = mb * 32 + c32;
+        const int kc = 2 * j + h;
+        const int phys = row * 8 + (kc ^ (row & 7));
+#pragma unroll
+        for (int p = 0; p < APLANES; p++) {
+          const half8_t af = ((const half8_t*)As[buf][p])[phys];
+#pragma unroll
+          for (int b = 0; b < 2; b++)
+            acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[b], acc[mb][b], 0, 0, 0);
+        }
+      }
+    }
+    if (more) store_a(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    if (more) {
+#pragma unroll
+      for (int b = 0; b < 2; b++) bcur[b] = bnext[b];
+    }
+  }
+
+  // Epilogue. Lane holds D[8*(r/4) + 4*h + (r%4)][c32] of each 32x32 block.
+  const bool split = gridDim.z > 1;
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (row >= g.M) continue;
+      if (split) {
+        float* dst = g.part + ((size_t)blockIdx.z * g.M + row) * g.N;
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+          if (nbv[b]) dst[(nbw0 + b) * 32 + c32] = acc[mb][b][r];
+      } else if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+        if (nbv[1]) {
+          const float v = silu_f(acc[mb][0][r]) * acc[mb][1][r];
+          const int col = (nbw0 >> 1) * 32 + c32;
+          const size_t o = (size_t)row * (g.N / 2) + col;
+          if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[o] = (half_t)v;
+          else ((float*)g.y)[o] = v;
+        }
+      } else {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          if (!nbv[b]) continue;
+          const size_t o = (size_t)row * g.N + (nbw0 + b) * 32 + c32;
+          if (EPI == EPI_F32) ((float*)g.y)[o] = acc[mb][b][r];
+          else if (EPI == EPI_F16) ((half_t*)g.y)[o] = (half_t)acc[mb][b][r];
+          else ((float*)g.y)[o] += acc[mb][b][r];
+        }
+      }
+    }
+  }
+}
+
+// Sums split-K partials in split order and applies the epilogue.
+template <int EPI>
+__global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
+  const int outN = (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) ? g.N / 2 : g.N;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)g.M * outN) return;
+  const int row = (int)(i / outN), col = (int)(i % outN);
+  const size_t plane = (size_t)g.M * g.N;
+  if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+    const int gc = (col / 32) * 64 + (col % 32), uc = gc + 32;
+    float ga = 0.f, ua = 0.f;
+    for (int s = 0; s < splits; s++) {
+      ga += g.part[s * plane + (size_t)row * g.N + gc];
+      ua += g.part[s * plane + (size_t)row * g.N + uc];
+    }
+    const float v = silu_f(ga) * ua;
+    if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[i] = (half_t)v;
+    else ((float*)g.y)[i] = v;
+  } else {
+    float a = 0.f;
+    for (int s = 0; s < splits; s++) a += g.part[s * plane + i];
+    if (EPI == EPI_F32) ((float*)g.y)[i] = a;
+    else if (EPI == EPI_F16) ((half_t*)g.y)[i] = (half_t)a;
+    else ((float*)g.y)[i] += a;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// repack: canonical host forms (already on the device) -> fragment-major
+// ---------------------------------------------------------------------------
+struct RepackArgs {
+  const void* plane;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  void* wp;
+  uint16_t* ws;
+  uint16_t* wz;
+  int K, N;            // the sub-weight's shape
+  int nb_stride, nb_off;  // its n-block nb lands at nb*nb_stride + nb_off
+};
+
+__device__ __forceinline__ int nib_slot(int e) { return (e & 1) * 4 + (e >> 1); }
+__device__ __forceinline__ int byte_slot(int e) { return (e & 1) * 2 + (e >> 1); }  // 0,2,1,3
+
+// One thread per (nb, ks, lane).
+template <int FORM>
+__global__ void repack_kernel(RepackArgs a) {
+  const int KS = a.K / 64, NBT = a.N / 32;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)NBT * KS * 64) return;
+  const int lane = (int)(t % 64), ks = (int)((t / 64) % KS), nb = (int)(t / 64 / KS);
+  const int h = lane >> 5, n = nb * 32 + (lane & 31);
+  const size_t N = (size_t)a.N;
+  const int onb = nb * a.nb_stride + a.nb_off;
+  const size_t ot = ((size_t)onb * KS + ks) * 64 + lane;  // output slot
+  for (int j = 0; j < 4; j++) {
+    const int kb = ks * 64 + 16 * j + 8 * h;
+    if (FORM == TGOHIP_FORM_F16) {
+      uint16_t* dst = (uint16_t*)a.wp + ot * 32 + j * 8;
+      for (int e = 0; e < 8; e++) dst[e] = ((const uint16_t*)a.plane)[(size_t)(kb + e) * N + n];
+    } else if (FORM == TGOHIP_FORM_I4_SYM) {
+      uint32_t w = 0;
+      for (int e = 0; e < 8; e++) {
+        const int k = kb + e;
+        const uint32_t word = ((const uint32_t*)a.plane)[(size_t)(k / 8) * N + n];
+        w |= ((word >> (4 * (k % 8))) & 15u) << (4 * nib_slot(e));
+      }
+      ((uint32_t*)a.wp)[ot * 4 + j] = w;
+    } else if (FORM == TGOHIP_FORM_I4_TGO) {
+      uint32_t w = 0;
+      for (int e = 0; e < 8; e++) {
+        const size_t i = (size_t)(kb + e) * N + n;
+        const uint32_t q = (((const uint32_t*)a.plane)[i / 8] >> (4 * (i % 8))) & 15u;
+        w |= q << (4 * nib_slot(e));
+      }
+      ((uint32_t*)a.wp)[ot * 4 + j] = w;
+    } else {
+      uint32_t w[2] = {0, 0};
+      for (int e = 0; e < 8; e++) {
+        const size_t i = (size_t)(kb + e) * N + n;
+        const uint32_t b = (uint32_t)((int)((const int8_t*)a.plane)[i] + 128) & 255u;
+        w[e >> 2] |= b << (8 * byte_slot(e & 3));
+      }
+      ((uint32_t*)a.wp)[ot * 8 + j * 2] = w[0];
+      ((uint32_t*)a.wp)[ot * 8 + j * 2 + 1] = w[1];
+    }
+    // per-k scales (and zeros) for I8 / I4_TGO: written by lanes 0 and 32.
+    if ((FORM == TGOHIP_FORM_I8 || FORM == TGOHIP_FORM_I4_TGO) && (lane & 31) == 0) {
+      const size_t o = ((((size_t)onb * KS + ks) * 4 + j) * 2 + h) * 8;
+      for (int e = 0; e < 8; e++) {
+        const size_t i = (size_t)(kb + e) * N + n;  // n is the block's first column
+        if (FORM == TGOHIP_FORM_I8) {
+          a.ws[o + e] = a.scales[i / 32];
+        } else {
+          a.ws[o + e] = a.scales[i / 128];
+          // 1024 + z, exact in f16 for an integer zero in [0, 1023]
+          const float z = (float)(*(const half_t*)&a.zeros[i / 128]);
+          const half_t zz = (half_t)(1024.f + z);
+          a.wz[o + e] = *(const uint16_t*)&zz;
+        }
+      }
+    }
+  }
+  if (FORM == TGOHIP_FORM_I4_SYM && h == 0) {
+    const size_t o = (((size_t)onb * KS + ks) * 32 + (lane & 31)) * 2;
+    a.ws[o] = a.scales[(size_t)(2 * ks) * N + n];
+    a.ws[o + 1] = a.scales[(size_t)(2 * ks + 1) * N + n];
+  }
+}
+
+// Dequantizes a packed weight to [K,N]: f32 exactly ((q - z) * s in f32) or the
+// f16 the MFMA path multiplies (the same device functions as the GEMM).
+template <int FORM, bool F16OUT>
+__global__ void dequant_kernel(GemmArgs g, void* out) {
+  const int KS = g.K / 64, NBT = g.N / 32;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)NBT * KS * 64) return;
+  const int lane = (int)(t % 64), ks = (int)((t / 64) % KS), nb = (int)(t / 64 / KS);
+  const int h = lane >> 5, n = nb * 32 + (lane & 31);
+  BRaw<FORM> r;
+  load_braw<FORM>(g, nb, ks, lane, r);
+  for (int j = 0; j < 4; j++) {
+    const int kb = ks * 64 + 16 * j + 8 * h;
+    if (F16OUT) {
+      const half8_t f = bfrag<FORM>(r, j);
+      for (int e = 0; e < 8; e++) ((half_t*)out)[(size_t)(kb + e) * g.N + n] = f[e];
+    } else {
+      for (int e = 0; e < 8; e++) {
+        float v;
+        if (FORM == TGOHIP_FORM_F16) {
+          union { uint4 u; half8_t hh; } c;
+          c.u = r.p[j];
+          v = (float)c.hh[e];
+        } else if (FORM == TGOHIP_FORM_I4_SYM || FORM == TGOHIP_FORM_I4_TGO) {
+          const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
+          const uint32_t q = (w >> (4 * nib_slot(e))) & 15u;
+          if (FORM == TGOHIP_FORM_I4_SYM) {
+            union { uint32_t u; half2_t hh; } sc;
+            sc.u = r.s[0].x;
+            v = (float)((int)q - 8) * (float)(j < 2 ? sc.hh[0] : sc.hh[1]);
+          } else {
+            union { uint4 u; half8_t hh; } s, z;
+            s.u = r.s[j];
+            z.u = r.z[j];
+            v = ((float)q - ((float)z.hh[e] - 1024.f)) * (float)s.hh[e];
+          }
+        } else {
+          const uint4 qq = r.p[j >> 1];
+          const uint32_t w = (e < 4) ? ((j & 1) ? qq.z : qq.x) : ((j & 1) ? qq.w : qq.y);
+          const uint32_t b = (w >> (8 * byte_slot(e & 3))) & 255u;
+          union { uint4 u; half8_t hh; } s;
+          s.u = r.s[j];
+          v = (float)((int)b - 128) * (float)s.hh[e];
+        }
+        ((float*)out)[(size_t)(kb + e) * g.N + n] = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+size_t packed_payload_bytes(int form, int K, int N) {
+  const size_t slots = (size_t)(N / 32) * (K / 64) * 64;
+  switch (form) {
+    case TGOHIP_FORM_F16: return slots * 64;
+    case TGOHIP_FORM_I8: return slots * 32;
+    default: return slots * 16;
+  }
+}
+size_t packed_scale_halves(int form, int K, int N) {
+  switch (form) {
+    case TGOHIP_FORM_I4_SYM: return (size_t)(N / 32) * (K / 64) * 32 * 2;
+    case TGOHIP_FORM_I8:
+    case TGOHIP_FORM_I4_TGO: return (size_t)(N / 32) * (K / 64) * 4 * 2 * 8;
+    default: return 0;
+  }
+}
+
+int repack_enqueue(int form, const void* plane, const uint16_t* scales, const uint16_t* zeros,
+                   int K, int N, PackedWeight& w, int nb_stride, int nb_off, hipStream_t st) {
+  RepackArgs a{plane, scales, zeros, w.wp, (uint16_t*)w.ws, (uint16_t*)w.wz, K, N, nb_stride, nb_off};
+  const size_t threads = (size_t)(N / 32) * (K / 64) * 64;
+  const dim3 grid((unsigned)((threads + 255) / 256)), blk(256);
+  switch (form) {
+    case TGOHIP_FORM_F16: hipLaunchKernelGGL(repack_kernel<TGOHIP_FORM_F16>, grid, blk, 0, st, a); break;
+    case TGOHIP_FORM_I8: hipLaunchKernelGGL(repack_kernel<TGOHIP_FORM_I8>, grid, blk, 0, st, a); break;
+    case TGOHIP_FORM_I4_TGO: hipLaunchKernelGGL(repack_kernel<TGOHIP_FORM_I4_TGO>, grid, blk, 0, st, a); break;
+    case TGOHIP_FORM_I4_SYM: hipLaunchKernelGGL(repack_kernel<TGOHIP_FORM_I4_SYM>, grid, blk, 0, st, a); break;
+  }
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t st) {
+  GemmArgs g{};
+  g.wp = w.wp;
+  g.ws = w.ws;
+  g.wz = w.wz;
+  g.K = w.K;
+  g.N = w.N;
+  const size_t threads = (size_t)(w.N / 32) * (w.K / 64) * 64;
+  const dim3 grid((unsigned)((threads + 255) / 256)), blk(256);
+#define DQ(F)                                                                              \
+  if (f16out) hipLaunchKernelGGL((dequant_kernel<F, true>), grid, blk, 0, st, g, out);     \
+  else hipLaunchKernelGGL((dequant_kernel<F, false>), grid, blk, 0, st, g, out);
+  switch (w.form) {
+    case TGOHIP_FORM_F16: DQ(TGOHIP_FORM_F16); break;
+    case TGOHIP_FORM_I8: DQ(TGOHIP_FORM_I8); break;
+    case TGOHIP_FORM_I4_TGO: DQ(TGOHIP_FORM_I4_TGO); break;
+    case TGOHIP_FORM_I4_SYM: DQ(TGOHIP_FORM_I4_SYM); break;
+  }
+#undef DQ
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+// Split-K factor: enough workgroups to cover the chip twice, while each split
+// keeps at least four 64-deep steps.
+static int choose_splits(int M, int N, int K, int MW, int ncu) {
+  const int tiles = ((N / 32 + 7) / 8) * ((M + MW - 1) / MW);
+  const int KS = K / 64;
+  int s = 1;
+  while (tiles * s < 2 * ncu && KS / (s * 2) >= 4) s *= 2;
+  return s;
+}
+
+template <int FORM, int MW, bool ASPLIT>
+static void launch_form(const GemmArgs& g, int epi, dim3 grid, hipStream_t st) {
+  const dim3 blk(256);
+  switch (epi) {
+    case EPI_F32: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_F32>), grid, blk, 0, st, g); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_F16>), grid, blk, 0, st, g); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_RESID>), grid, blk, 0, st, g); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_SWIGLU_F16>), grid, blk, 0, st, g); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_SWIGLU_F32>), grid, blk, 0, st, g); break;
+  }
+}
+
+template <int MW, bool ASPLIT>
+static void launch_mw(int form, const GemmArgs& g, int epi, dim3 grid, hipStream_t st) {
+  switch (form) {
+    case TGOHIP_FORM_F16: launch_form<TGOHIP_FORM_F16, MW, ASPLIT>(g, epi, grid, st); break;
+    case TGOHIP_FORM_I8: launch_form<TGOHIP_FORM_I8, MW, ASPLIT>(g, epi, grid, st); break;
+    case TGOHIP_FORM_I4_TGO: launch_form<TGOHIP_FORM_I4_TGO, MW, ASPLIT>(g, epi, grid, st); break;
+    case TGOHIP_FORM_I4_SYM: launch_form<TGOHIP_FORM_I4_SYM, MW, ASPLIT>(g, epi, grid, st); break;
+  }
+}
+
+// Workspace bytes a call needs for split-K partials.
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
+  const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
+  const int s = choose_splits(M, w.N, w.K, MW, ncu);
+  return s > 1 ? (size_t)s * M * w.N * sizeof(float) : 0;
+}
+
+int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
+                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
+  if (M <= 0) return 0;
+  const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
+  const int splits = choose_splits(M, w.N, w.K, MW, ncu);
+  GemmArgs g{};
+  g.x = x;
+  g.wp = w.wp;
+  g.ws = w.ws;
+  g.wz = w.wz;
+  g.y = y;
+  g.M = M;
+  g.K = w.K;
+  g.N = w.N;
+  const int KS = w.K / 64;
+  g.ksteps_per_split = (KS + splits - 1) / splits;
+  if (splits > 1) {
+    if (!workspace || ws_bytes < (size_t)splits * M * w.N * sizeof(float))
+      return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
+    g.part = workspace;
+  }
+  const dim3 grid((unsigned)((w.N / 32 + 7) / 8), (unsigned)((M + MW - 1) / MW), (unsigned)splits);
+  if (MW == 32) {
+    if (x_f32) launch_mw<32, true>(w.form, g, epi, grid, st);
+    else launch_mw<32, false>(w.form, g, epi, grid, st);
+  } else if (MW == 64) {
+    if (x_f32) launch_mw<64, true>(w.form, g, epi, grid, st);
+    else launch_mw<64, false>(w.form, g, epi, grid, st);
+  } else {
+    if (x_f32) launch_mw<128, true>(w.form, g, epi, grid, st);
+    else launch_mw<128, false>(w.form, g, epi, grid, st);
+  }
+  if (splits > 1) {
+    const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? w.N / 2 : w.N;
+    const size_t total = (size_t)M * outN;
+    const dim3 rg((unsigned)((total + 255) / 256)), rb(256);
+    switch (epi) {
+      case EPI_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F32>, rg, rb, 0, st, g, splits); break;
+      case EPI_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F16>, rg, rb, 0, st, g, splits); break;
+      case EPI_RESID: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RESID>, rg, rb, 0, st, g, splits); break;
+      case EPI_SWIGLU_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F16>, rg, rb, 0, st, g, splits); break;
+      case EPI_SWIGLU_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F32>, rg, rb, 0, st, g, splits); break;
+    }
+  }
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // namespace tgohip

@@ -1,0 +1,1156 @@
+// runtime.hip -- the C ABI of libtgohip: context, weight upload and repack,
+// KV pool, the batched step (Batch.step, batch.go:314-458), the op-level entry
+// points, and the Scheduler (scheduler.go) driving it.
+#include "common.h"
+#include "host/hostlogic.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+extern uint16_t tgohip_f16_bits(float x, int* saturated);
+
+namespace tgohip {
+
+static thread_local std::string g_err;
+void set_error(const std::string& m) { g_err = m; }
+int fail(int code, const std::string& m) {
+  g_err = m;
+  return code;
+}
+std::string hip_message(hipError_t e, const char* what) {
+  return std::string("hip: ") + what + ": " + hipGetErrorString(e);
+}
+
+// Grow-only device buffer.
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  int ensure(size_t n) {
+    if (n <= bytes) return 0;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+    hipError_t e = hipMalloc(&p, n);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return fail(TGOHIP_ENOMEM, "device allocation of " + std::to_string(n) + " bytes: " +
+                                     hipGetErrorString(e));
+    }
+    bytes = n;
+    return 0;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+struct Layer {
+  PackedWeight qkv, wo, gateup, down;
+  float* g_attn = nullptr;
+  float* g_ffn = nullptr;
+  float* g_q = nullptr;
+  float* g_k = nullptr;
+};
+
+}  // namespace tgohip
+
+using namespace tgohip;
+
+struct tgohip_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  int ncu = 256;
+  bool configured = false;
+  tgohip_model_cfg cfg{};
+  std::vector<Layer> layers;
+  void* embed = nullptr;
+  uint16_t* embed_scales = nullptr;
+  int embed_form = -1;
+  PackedWeight lm_head;
+  float* g_final = nullptr;
+  double* inv_freq = nullptr;
+  half_t* kc = nullptr;
+  half_t* vc = nullptr;
+  int kv_positions = 0;
+  int precision = 0;  // 0: f16 activations into MFMA, 1: f32 activations (hi+lo)
+  // activations and workspaces
+  DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, meta, gemm_ws, part_o, part_ml;
+  int rows_cap = 0, batch_cap = 0;
+  // pinned staging for per-step metadata
+  void* pinned = nullptr;
+  size_t pinned_bytes = 0;
+  hipEvent_t staged = nullptr;  // the last H2D copy out of `pinned`
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  std::vector<void*> allocs;  // weight and gain allocations owned by the context
+  std::map<int, PackedWeight> handles;
+  int next_handle = 1;
+};
+
+namespace {
+
+int alloc_owned(tgohip_ctx* c, void** p, size_t bytes) {
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess)
+    return fail(TGOHIP_ENOMEM, "device allocation of " + std::to_string(bytes) + " bytes: " +
+                                   hipGetErrorString(e));
+  c->allocs.push_back(*p);
+  return 0;
+}
+
+void free_owned(tgohip_ctx* c, void* p) {
+  if (!p) return;
+  auto it = std::find(c->allocs.begin(), c->allocs.end(), p);
+  if (it != c->allocs.end()) c->allocs.erase(it);
+  (void)hipFree(p);
+}
+
+int ensure_pinned(tgohip_ctx* c, size_t bytes) {
+  if (c->staged) TGOHIP_HIP(hipEventSynchronize(c->staged));
+  if (bytes <= c->pinned_bytes) return 0;
+  if (c->pinned) (void)hipHostFree(c->pinned);
+  c->pinned = nullptr;
+  c->pinned_bytes = 0;
+  TGOHIP_HIP(hipHostMalloc(&c->pinned, bytes, hipHostMallocDefault));
+  c->pinned_bytes = bytes;
+  return 0;
+}
+
+// Metadata packer: appends arrays into the pinned staging buffer at 256-byte
+// aligned offsets, then one H2D copy moves all of them into c->meta.
+struct Stager {
+  std::vector<std::pair<const void*, size_t>> parts;
+  std::vector<size_t> offs;
+  size_t total = 0;
+  size_t add(const void* p, size_t bytes) {
+    const size_t o = total;
+    parts.push_back({p, bytes});
+    offs.push_back(o);
+    total += (bytes + 255) / 256 * 256;
+    return o;
+  }
+  int upload(tgohip_ctx* c) {
+    if (total == 0) return 0;
+    int rc = ensure_pinned(c, total);
+    if (rc) return rc;
+    rc = c->meta.ensure(total);
+    if (rc) return rc;
+    for (size_t i = 0; i < parts.size(); i++)
+      if (parts[i].second) memcpy((char*)c->pinned + offs[i], parts[i].first, parts[i].second);
+    TGOHIP_HIP(hipMemcpyAsync(c->meta.p, c->pinned, total, hipMemcpyHostToDevice, c->stream));
+    TGOHIP_HIP(hipEventRecord(c->staged, c->stream));
+    return 0;
+  }
+  template <class T> T* dev(tgohip_ctx* c, size_t off) { return (T*)((char*)c->meta.p + off); }
+};
+
+int check_shape(int form, int K, int N, const char* what) {
+  if (form < TGOHIP_FORM_F16 || form > TGOHIP_FORM_I4_SYM)
+    return fail(TGOHIP_EINVAL, std::string(what) + ": form " + std::to_string(form) +
+                                   " is not f16, int8, int4 or the symmetric int4 pack");
+  if (K <= 0 || N <= 0 || K % 64 != 0 || N % 32 != 0)
+    return fail(TGOHIP_EINVAL, std::string(what) + " is [" + std::to_string(K) + "," +
+                                   std::to_string(N) + "]; this library takes K a multiple of 64 "
+                                   "and N a multiple of 32");
+  if (form == TGOHIP_FORM_I4_TGO && N % 128 != 0)
+    return fail(TGOHIP_EINVAL, std::string(what) + ": the int4 triple groups 128 flattened "
+                                   "elements and N " + std::to_string(N) +
+                                   " is not a multiple of 128, so a group would straddle rows");
+  return 0;
+}
+
+size_t scale_count(int form, int K, int N) {
+  const size_t n = (size_t)K * N;
+  switch (form) {
+    case TGOHIP_FORM_I8: return (n + 31) / 32;
+    case TGOHIP_FORM_I4_TGO: return (n + 127) / 128;
+    case TGOHIP_FORM_I4_SYM: return (size_t)(K / 32) * N;
+  }
+  return 0;
+}
+size_t plane_bytes(int form, int K, int N) {
+  const size_t n = (size_t)K * N;
+  switch (form) {
+    case TGOHIP_FORM_F16: return n * 2;
+    case TGOHIP_FORM_I8: return n;
+    case TGOHIP_FORM_I4_TGO: return (n + 7) / 8 * 4;
+    case TGOHIP_FORM_I4_SYM: return n / 2;
+  }
+  return 0;
+}
+
+// Allocates w as a packed [K, N] weight of `form`.
+int alloc_packed(tgohip_ctx* c, PackedWeight& w, int form, int K, int N) {
+  w.form = form;
+  w.K = K;
+  w.N = N;
+  int rc = alloc_owned(c, &w.wp, packed_payload_bytes(form, K, N));
+  if (rc) return rc;
+  const size_t sh = packed_scale_halves(form, K, N);
+  w.ws = nullptr;
+  w.wz = nullptr;
+  if (sh) {
+    rc = alloc_owned(c, (void**)&w.ws, sh * 2);
+    if (rc) return rc;
+  }
+  if (form == TGOHIP_FORM_I4_TGO) {
+    rc = alloc_owned(c, (void**)&w.wz, sh * 2);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+void free_packed(tgohip_ctx* c, PackedWeight& w) {
+  free_owned(c, w.wp);
+  free_owned(c, w.ws);
+  free_owned(c, w.wz);
+  w = PackedWeight();
+}
+
+// Canonical (host-layout) weight resident on the device, temporary.
+struct Canon {
+  void* plane = nullptr;
+  uint16_t* scales = nullptr;
+  uint16_t* zeros = nullptr;
+  ~Canon() {
+    if (plane) (void)hipFree(plane);
+    if (scales) (void)hipFree(scales);
+    if (zeros) (void)hipFree(zeros);
+  }
+};
+
+int canon_alloc(Canon& cn, int form, int K, int N) {
+  TGOHIP_HIP(hipMalloc(&cn.plane, plane_bytes(form, K, N)));
+  const size_t sc = scale_count(form, K, N);
+  if (sc) TGOHIP_HIP(hipMalloc((void**)&cn.scales, sc * 2));
+  if (form == TGOHIP_FORM_I4_TGO) TGOHIP_HIP(hipMalloc((void**)&cn.zeros, sc * 2));
+  return 0;
+}
+
+int canon_upload(tgohip_ctx* c, Canon& cn, int form, int K, int N, const void* plane,
+                 const void* scales, const void* zeros) {
+  int rc = canon_alloc(cn, form, K, N);
+  if (rc) return rc;
+  if (!plane) return fail(TGOHIP_EINVAL, "weight: the plane is missing");
+  TGOHIP_HIP(hipMemcpyAsync(cn.plane, plane, plane_bytes(form, K, N), hipMemcpyHostToDevice, c->stream));
+  const size_t sc = scale_count(form, K, N);
+  if (sc) {
+    if (!scales) return fail(TGOHIP_EINVAL, "weight: a quantized form carries scales");
+    TGOHIP_HIP(hipMemcpyAsync(cn.scales, scales, sc * 2, hipMemcpyHostToDevice, c->stream));
+  }
+  if (form == TGOHIP_FORM_I4_TGO) {
+    if (!zeros) return fail(TGOHIP_EINVAL, "weight: the int4 triple carries zeros");
+    TGOHIP_HIP(hipMemcpyAsync(cn.zeros, zeros, sc * 2, hipMemcpyHostToDevice, c->stream));
+  }
+  return 0;
+}
+
+// Synthesises a canonical weight on the device (the CPU restatement's
+// generator: oracle.c synth_weight).
+int canon_synth(tgohip_ctx* c, Canon& cn, uint64_t seed, uint64_t stream, int form, int K, int N,
+                double sigma) {
+  int rc = canon_alloc(cn, form, K, N);
+  if (rc) return rc;
+  const size_t n = (size_t)K * N, sc = scale_count(form, K, N);
+  hipStream_t st = c->stream;
+  switch (form) {
+    case TGOHIP_FORM_F16: launch_synth_f16(seed, stream * 4, n, sigma, (uint16_t*)cn.plane, st); break;
+    case TGOHIP_FORM_I8:
+      launch_synth_i8(seed, stream * 4, n, (int8_t*)cn.plane, st);
+      launch_synth_absf16(seed, stream * 4 + 1, sc, sigma / 64.0, cn.scales, st);
+      break;
+    case TGOHIP_FORM_I4_TGO:
+      launch_synth_i4tgo(seed, stream * 4, n, (uint32_t*)cn.plane, st);
+      launch_synth_absf16(seed, stream * 4 + 1, sc, sigma / 4.0, cn.scales, st);
+      launch_synth_zero(seed, stream * 4 + 2, sc, cn.zeros, st);
+      break;
+    case TGOHIP_FORM_I4_SYM:
+      launch_synth_i4sym(seed, stream * 4, K, N, (uint32_t*)cn.plane, st);
+      launch_synth_absf16(seed, stream * 4 + 1, sc, sigma / 4.0, cn.scales, st);
+      break;
+  }
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+enum PortKind { P_EMBED, P_LMHEAD, P_WQ, P_WK, P_WV, P_WO, P_WGATE, P_WUP, P_WDOWN, P_BAD };
+
+PortKind parse_port(const char* port, int& layer) {
+  layer = -1;
+  if (!strcmp(port, "embed")) return P_EMBED;
+  if (!strcmp(port, "lm_head")) return P_LMHEAD;
+  char* end = nullptr;
+  const long l = strtol(port, &end, 10);
+  if (end == port || *end != '.') return P_BAD;
+  layer = (int)l;
+  const char* name = end + 1;
+  static const std::pair<const char*, PortKind> names[] = {
+      {"wq", P_WQ}, {"wk", P_WK}, {"wv", P_WV}, {"wo", P_WO},
+      {"wgate", P_WGATE}, {"wup", P_WUP}, {"wdown", P_WDOWN}};
+  for (auto& p : names)
+    if (!strcmp(name, p.first)) return p.second;
+  return P_BAD;
+}
+
+// Places one port's canonical device weight into the context's packed layout.
+int place_weight(tgohip_ctx* c, PortKind kind, int l, int form, int K, int N, const Canon& cn,
+                 const char* port) {
+  const tgohip_model_cfg& m = c->cfg;
+  const int d = m.hidden, qw = m.heads * m.head_dim, kw = m.kv_heads * m.head_dim, f = m.ffn;
+  int wantK = 0, wantN = 0;
+  switch (kind) {
+    case P_LMHEAD: wantK = d; wantN = m.vocab; break;
+    case P_WQ: wantK = d; wantN = qw; break;
+    case P_WK: case P_WV: wantK = d; wantN = kw; break;
+    case P_WO: wantK = qw; wantN = d; break;
+    case P_WGATE: case P_WUP: wantK = d; wantN = f; break;
+    case P_WDOWN: wantK = f; wantN = d; break;
+    default: break;
+  }
+  if (K != wantK || N != wantN)
+    return fail(TGOHIP_EINVAL, std::string("weight ") + port + " is [" + std::to_string(K) + "," +
+                                   std::to_string(N) + "] and the config asks for [" +
+                                   std::to_string(wantK) + "," + std::to_string(wantN) + "]");
+  int rc = check_shape(form, K, N, port);
+  if (rc) return rc;
+  PackedWeight* w = nullptr;
+  int fusedN = N, stride = 1, off = 0;
+  if (kind == P_LMHEAD) {
+    w = &c->lm_head;
+  } else {
+    Layer& L = c->layers[l];
+    switch (kind) {
+      case P_WQ: w = &L.qkv; fusedN = qw + 2 * kw; off = 0; break;
+      case P_WK: w = &L.qkv; fusedN = qw + 2 * kw; off = qw / 32; break;
+      case P_WV: w = &L.qkv; fusedN = qw + 2 * kw; off = (qw + kw) / 32; break;
+      case P_WO: w = &L.wo; break;
+      case P_WGATE: w = &L.gateup; fusedN = 2 * f; stride = 2; off = 0; break;
+      case P_WUP: w = &L.gateup; fusedN = 2 * f; stride = 2; off = 1; break;
+      case P_WDOWN: w = &L.down; break;
+      default: break;
+    }
+  }
+  if (w->form >= 0 && w->form != form) {
+    if (fusedN != N)
+      return fail(TGOHIP_EINVAL, std::string("weight ") + port + " is form " + std::to_string(form) +
+                                     " and the projection it is fused with is form " +
+                                     std::to_string(w->form) + "; fused projections share a form");
+    free_packed(c, *w);
+  }
+  if (w->form < 0) {
+    rc = alloc_packed(c, *w, form, K, fusedN);
+    if (rc) return rc;
+  }
+  return repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, *w, stride, off, c->stream);
+}
+
+int ensure_activations(tgohip_ctx* c, int rows, int B) {
+  const tgohip_model_cfg& m = c->cfg;
+  const size_t d = m.hidden, qw = (size_t)m.heads * m.head_dim, kw = (size_t)m.kv_heads * m.head_dim;
+  const size_t f = m.ffn;
+  const size_t act_el = c->precision ? 4 : 2;
+  int rc = 0;
+  if (rows > c->rows_cap) {
+    if ((rc = c->h.ensure(rows * d * 4))) return rc;
+    if ((rc = c->xn.ensure(rows * d * 4))) return rc;
+    if ((rc = c->qkv.ensure(rows * (qw + 2 * kw) * 4))) return rc;
+    if ((rc = c->q.ensure(rows * qw * 4))) return rc;
+    if ((rc = c->attn.ensure(rows * qw * 4))) return rc;
+    if ((rc = c->act.ensure(rows * f * act_el + 256))) return rc;
+    c->rows_cap = rows;
+  }
+  if (B > c->batch_cap) {
+    if ((rc = c->lastn.ensure((size_t)B * d * 4))) return rc;
+    if ((rc = c->logits.ensure((size_t)B * m.vocab * 4))) return rc;
+    if ((rc = c->argmax.ensure((size_t)B * 4))) return rc;
+    c->batch_cap = B;
+  }
+  // split-K workspace: the largest any projection of this step may ask for
+  size_t ws = 0;
+  for (const Layer& L : c->layers)
+    for (const PackedWeight* w : {&L.qkv, &L.wo, &L.gateup, &L.down})
+      if (w->form >= 0) ws = std::max(ws, gemm_workspace_bytes(*w, rows, c->ncu));
+  if (c->lm_head.form >= 0) ws = std::max(ws, gemm_workspace_bytes(c->lm_head, B, c->ncu));
+  if ((rc = c->gemm_ws.ensure(ws + 256))) return rc;
+  return 0;
+}
+
+int ensure_attn_parts(tgohip_ctx* c, int parts) {
+  int rc = c->part_o.ensure((size_t)std::max(parts, 1) * 16 * 128 * 4);
+  if (rc) return rc;
+  return c->part_ml.ensure((size_t)std::max(parts, 1) * 32 * 4);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* tgohip_last_error(void) { return g_err.c_str(); }
+const char* tgohip_version(void) { return "tgohip 0.1 gfx950"; }
+
+tgohip_ctx* tgohip_open(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    fail(TGOHIP_EDEVICE, "tgohip_open: no HIP device is visible");
+    return nullptr;
+  }
+  if (device < 0 || device >= n) {
+    fail(TGOHIP_EINVAL, "tgohip_open: device " + std::to_string(device) + " of " + std::to_string(n));
+    return nullptr;
+  }
+  if (hipSetDevice(device) != hipSuccess) {
+    fail(TGOHIP_EDEVICE, "tgohip_open: hipSetDevice failed");
+    return nullptr;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+    fail(TGOHIP_EDEVICE, "tgohip_open: hipGetDeviceProperties failed");
+    return nullptr;
+  }
+  if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos) {
+    fail(TGOHIP_EDEVICE, std::string("tgohip_open: this library is built for gfx950 and the device is ") +
+                             prop.gcnArchName);
+    return nullptr;
+  }
+  auto* c = new tgohip_ctx();
+  c->device = device;
+  c->ncu = prop.multiProcessorCount;
+  if (hipStreamCreate(&c->own_stream) != hipSuccess ||
+      hipEventCreateWithFlags(&c->staged, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+    fail(TGOHIP_EDEVICE, "tgohip_open: stream/event creation failed");
+    delete c;
+    return nullptr;
+  }
+  c->stream = c->own_stream;
+  return c;
+}
+
+void tgohip_close(tgohip_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (void* p : c->allocs) (void)hipFree(p);
+  c->allocs.clear();
+  for (DevBuf* b : {&c->h, &c->xn, &c->qkv, &c->q, &c->attn, &c->act, &c->lastn, &c->logits,
+                    &c->argmax, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml})
+    b->release();
+  if (c->kc) (void)hipFree(c->kc);
+  if (c->vc) (void)hipFree(c->vc);
+  if (c->pinned) (void)hipHostFree(c->pinned);
+  (void)hipEventDestroy(c->staged);
+  (void)hipEventDestroy(c->ev0);
+  (void)hipEventDestroy(c->ev1);
+  (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+void* tgohip_stream(tgohip_ctx* c) { return (void*)c->stream; }
+
+// Launch on a caller's stream (for instance torch's current stream) instead
+// of the context's own. NULL is the device's default stream.
+int tgohip_set_stream(tgohip_ctx* c, void* stream) {
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  c->stream = (hipStream_t)stream;
+  return 0;
+}
+
+int tgohip_use_own_stream(tgohip_ctx* c) {
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  c->stream = c->own_stream;
+  return 0;
+}
+
+int tgohip_sync(tgohip_ctx* c) {
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+int tgohip_set_precision(tgohip_ctx* c, int mode) {
+  if (mode != 0 && mode != 1) return fail(TGOHIP_EINVAL, "precision is 0 (f16 activations) or 1 (f32 activations)");
+  c->precision = mode;
+  c->rows_cap = 0;  // activation dtype changed: regrow
+  return 0;
+}
+
+int tgohip_config(tgohip_ctx* c, const tgohip_model_cfg* m) {
+  if (c->configured) return fail(TGOHIP_ESTATE, "config: the context is already configured");
+  if (m->layers <= 0 || m->hidden <= 0 || m->heads <= 0 || m->kv_heads <= 0 || m->vocab <= 0 ||
+      m->ffn <= 0)
+    return fail(TGOHIP_EINVAL, "config: every dimension is positive");
+  if (m->head_dim != kHeadDim)
+    return fail(TGOHIP_EINVAL, "config: head_dim is " + std::to_string(m->head_dim) +
+                                   "; the kernels are built for 128 (every Qwen3 size)");
+  if (m->heads % m->kv_heads != 0)
+    return fail(TGOHIP_EINVAL, "config: num_attention_heads " + std::to_string(m->heads) +
+                                   " is not a multiple of num_key_value_heads " +
+                                   std::to_string(m->kv_heads));
+  if (m->hidden % 64 != 0 || m->ffn % 64 != 0 || m->vocab % 32 != 0)
+    return fail(TGOHIP_EINVAL, "config: hidden and ffn are multiples of 64 and vocab of 32");
+  if (m->block <= 0) return fail(TGOHIP_EINVAL, "config: block is " + std::to_string(m->block));
+  if (!(m->rms_eps > 0)) return fail(TGOHIP_EINVAL, "config: rms_norm_eps must be positive");
+  c->cfg = *m;
+  c->layers.assign(m->layers, Layer());
+  // theta_i = base^(-2i/d_h) in double, once (internal/oracle/rope.go:119).
+  std::vector<double> inv(kHeadDim / 2);
+  for (int i = 0; i < kHeadDim / 2; i++)
+    inv[i] = std::pow((double)m->rope_theta, -2.0 * (double)i / (double)kHeadDim);
+  int rc = alloc_owned(c, (void**)&c->inv_freq, inv.size() * sizeof(double));
+  if (rc) return rc;
+  TGOHIP_HIP(hipMemcpy(c->inv_freq, inv.data(), inv.size() * sizeof(double), hipMemcpyHostToDevice));
+  c->configured = true;
+  return 0;
+}
+
+int tgohip_weight(tgohip_ctx* c, const char* port, int form, int K, int N, const void* plane,
+                  const void* scales, const void* zeros) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "weight: configure the context first");
+  int l;
+  const PortKind kind = parse_port(port, l);
+  if (kind == P_BAD || (l >= 0 && l >= c->cfg.layers))
+    return fail(TGOHIP_EINVAL, std::string("weight: no port named ") + port);
+  if (kind == P_EMBED) {
+    if (form != TGOHIP_FORM_F16 && form != TGOHIP_FORM_I8)
+      return fail(TGOHIP_EINVAL, "weight embed: the embedding is gathered by row and is f16 or int8 "
+                                 "(weights/weights.go:543-545 caps int4 to int8)");
+    if (K != c->cfg.vocab || N != c->cfg.hidden)
+      return fail(TGOHIP_EINVAL, "weight embed is [" + std::to_string(K) + "," + std::to_string(N) +
+                                     "] and the config asks for [vocab, hidden]");
+    free_owned(c, c->embed);
+    free_owned(c, c->embed_scales);
+    c->embed_scales = nullptr;
+    int rc = alloc_owned(c, &c->embed, plane_bytes(form, K, N));
+    if (rc) return rc;
+    TGOHIP_HIP(hipMemcpy(c->embed, plane, plane_bytes(form, K, N), hipMemcpyHostToDevice));
+    if (form == TGOHIP_FORM_I8) {
+      rc = alloc_owned(c, (void**)&c->embed_scales, scale_count(form, K, N) * 2);
+      if (rc) return rc;
+      TGOHIP_HIP(hipMemcpy(c->embed_scales, scales, scale_count(form, K, N) * 2, hipMemcpyHostToDevice));
+    }
+    c->embed_form = form;
+    return 0;
+  }
+  int rc = check_shape(form, K, N, port);
+  if (rc) return rc;
+  Canon cn;
+  rc = canon_upload(c, cn, form, K, N, plane, scales, zeros);
+  if (rc) return rc;
+  rc = place_weight(c, kind, l, form, K, N, cn, port);
+  if (rc) return rc;
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+int tgohip_gain(tgohip_ctx* c, const char* port, const float* g, int width) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "gain: configure the context first");
+  float** dst = nullptr;
+  int want = 0;
+  if (!strcmp(port, "final_norm")) {
+    dst = &c->g_final;
+    want = c->cfg.hidden;
+  } else {
+    char* end = nullptr;
+    const long l = strtol(port, &end, 10);
+    if (end == port || *end != '.' || l < 0 || l >= c->cfg.layers)
+      return fail(TGOHIP_EINVAL, std::string("gain: no port named ") + port);
+    const char* name = end + 1;
+    Layer& L = c->layers[l];
+    if (!strcmp(name, "attn_norm")) { dst = &L.g_attn; want = c->cfg.hidden; }
+    else if (!strcmp(name, "ffn_norm")) { dst = &L.g_ffn; want = c->cfg.hidden; }
+    else if (!strcmp(name, "qnorm")) { dst = &L.g_q; want = kHeadDim; }
+    else if (!strcmp(name, "knorm")) { dst = &L.g_k; want = kHeadDim; }
+    else return fail(TGOHIP_EINVAL, std::string("gain: no port named ") + port);
+  }
+  if (width != want)
+    return fail(TGOHIP_EINVAL, std::string("gain ") + port + " is " + std::to_string(width) +
+                                   " wide and the config asks for " + std::to_string(want));
+  if (!*dst) {
+    int rc = alloc_owned(c, (void**)dst, (size_t)want * 4);
+    if (rc) return rc;
+  }
+  TGOHIP_HIP(hipMemcpy(*dst, g, (size_t)want * 4, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int tgohip_synth_weights(tgohip_ctx* c, uint64_t seed, int form, double sigma) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "synth: configure the context first");
+  const tgohip_model_cfg& m = c->cfg;
+  const int d = m.hidden, qw = m.heads * m.head_dim, kw = m.kv_heads * m.head_dim, f = m.ffn;
+  int rc;
+  // embedding: F16 under F16, else int8 (stream 1)
+  {
+    const int ef = form == TGOHIP_FORM_F16 ? TGOHIP_FORM_F16 : TGOHIP_FORM_I8;
+    free_owned(c, c->embed);
+    free_owned(c, c->embed_scales);
+    c->embed_scales = nullptr;
+    if ((rc = alloc_owned(c, &c->embed, plane_bytes(ef, m.vocab, d)))) return rc;
+    const size_t n = (size_t)m.vocab * d;
+    if (ef == TGOHIP_FORM_F16) {
+      launch_synth_f16(seed, 1 * 4, n, sigma, (uint16_t*)c->embed, c->stream);
+    } else {
+      if ((rc = alloc_owned(c, (void**)&c->embed_scales, scale_count(ef, m.vocab, d) * 2))) return rc;
+      launch_synth_i8(seed, 1 * 4, n, (int8_t*)c->embed, c->stream);
+      launch_synth_absf16(seed, 1 * 4 + 1, scale_count(ef, m.vocab, d), sigma / 64.0, c->embed_scales, c->stream);
+    }
+    c->embed_form = ef;
+  }
+  {
+    Canon cn;
+    if ((rc = check_shape(form, d, m.vocab, "lm_head"))) return rc;
+    if ((rc = canon_synth(c, cn, seed, 3, form, d, m.vocab, sigma))) return rc;
+    if ((rc = place_weight(c, P_LMHEAD, -1, form, d, m.vocab, cn, "lm_head"))) return rc;
+    TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  }
+  auto ones = [&](float** dst, int w) -> int {
+    if (!*dst) {
+      int r = alloc_owned(c, (void**)dst, (size_t)w * 4);
+      if (r) return r;
+    }
+    launch_fill_f32(*dst, (size_t)w, 1.0f, c->stream);
+    return 0;
+  };
+  if ((rc = ones(&c->g_final, d))) return rc;
+  struct P { PortKind k; int p; int K, N; const char* name; };
+  const P ports[] = {{P_WQ, 1, d, qw, "wq"}, {P_WK, 2, d, kw, "wk"}, {P_WV, 3, d, kw, "wv"},
+                     {P_WO, 4, qw, d, "wo"}, {P_WGATE, 8, d, f, "wgate"}, {P_WUP, 9, d, f, "wup"},
+                     {P_WDOWN, 10, f, d, "wdown"}};
+  for (int l = 0; l < m.layers; l++) {
+    Layer& L = c->layers[l];
+    if ((rc = ones(&L.g_attn, d)) || (rc = ones(&L.g_ffn, d)) || (rc = ones(&L.g_q, kHeadDim)) ||
+        (rc = ones(&L.g_k, kHeadDim)))
+      return rc;
+    for (const P& p : ports) {
+      Canon cn;
+      const std::string name = std::to_string(l) + "." + p.name;
+      if ((rc = check_shape(form, p.K, p.N, name.c_str()))) return rc;
+      if ((rc = canon_synth(c, cn, seed, (uint64_t)(l + 1) * 64 + p.p, form, p.K, p.N, sigma))) return rc;
+      if ((rc = place_weight(c, p.k, l, form, p.K, p.N, cn, name.c_str()))) return rc;
+      TGOHIP_HIP(hipStreamSynchronize(c->stream));
+    }
+  }
+  return 0;
+}
+
+int tgohip_kv_alloc(tgohip_ctx* c, int positions) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "kv_alloc: configure the context first");
+  const int blocks = positions / c->cfg.block;
+  if (blocks < 1)
+    return fail(TGOHIP_EINVAL, "kv_alloc: a shared cache of " + std::to_string(positions) +
+                                   " positions holds no whole block of " + std::to_string(c->cfg.block) +
+                                   "; it needs at least one");
+  const int pos = blocks * c->cfg.block;
+  const size_t n = (size_t)c->cfg.layers * pos * c->cfg.kv_heads * kHeadDim;
+  if (c->kc) (void)hipFree(c->kc);
+  if (c->vc) (void)hipFree(c->vc);
+  c->kc = c->vc = nullptr;
+  hipError_t e = hipMalloc((void**)&c->kc, n * 2);
+  if (e == hipSuccess) e = hipMalloc((void**)&c->vc, n * 2);
+  if (e != hipSuccess)
+    return fail(TGOHIP_ENOMEM, "kv_alloc: the shared prefix cache needs " + std::to_string(n * 2) +
+                                   " bytes per state at " + std::to_string(pos) +
+                                   " positions and the device refused it");
+  // Zeroed (blocks.go:117-137).
+  TGOHIP_HIP(hipMemsetAsync(c->kc, 0, n * 2, c->stream));
+  TGOHIP_HIP(hipMemsetAsync(c->vc, 0, n * 2, c->stream));
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  c->kv_positions = pos;
+  return 0;
+}
+
+int tgohip_kv_pointers(tgohip_ctx* c, void** k, void** v, int* positions) {
+  *k = c->kc;
+  *v = c->vc;
+  *positions = c->kv_positions;
+  return 0;
+}
+
+// ---- the batched step ------------------------------------------------------
+int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, int32_t* argmax_out,
+                tgohip_timings* tm) {
+  using clk = std::chrono::steady_clock;
+  const auto t_start = clk::now();
+  if (!c->configured) return fail(TGOHIP_ESTATE, "step: configure the context first");
+  if (!c->kc) return fail(TGOHIP_ESTATE, "step: a batched step needs a shared block pool (kv_alloc)");
+  const tgohip_model_cfg& m = c->cfg;
+  if (c->embed_form < 0 || c->lm_head.form < 0 || !c->g_final)
+    return fail(TGOHIP_ESTATE, "step: the embedding, lm_head and final_norm are bound first");
+  for (int l = 0; l < m.layers; l++) {
+    const Layer& L = c->layers[l];
+    if (L.qkv.form < 0 || L.wo.form < 0 || L.gateup.form < 0 || L.down.form < 0 || !L.g_attn ||
+        !L.g_ffn || !L.g_q || !L.g_k)
+      return fail(TGOHIP_ESTATE, "step: layer " + std::to_string(l) + " has an unbound port");
+  }
+  const int T = s->rows, B = s->batch;
+  if (T <= 0 || B <= 0) return fail(TGOHIP_EINVAL, "step: rows and batch are positive");
+  for (int t = 0; t < T; t++)
+    if (s->ids[t] >= (uint32_t)m.vocab)
+      return fail(TGOHIP_EINVAL, "step: row " + std::to_string(t) + " token id " +
+                                     std::to_string(s->ids[t]) + " is outside the vocabulary");
+  for (int b = 0; b < B; b++) {
+    if (s->extents[b] > 0 && s->last[b] >= (uint32_t)T)
+      return fail(TGOHIP_EINVAL, "step: member " + std::to_string(b) + " reads logits from row " +
+                                     std::to_string(s->last[b]) + " of " + std::to_string(T));
+  }
+  AttnPlan plan;
+  int rc = attn_build_plan(T, B, s->lengths, s->extents, s->pages, s->max_pages, m.block,
+                           c->kv_positions, m.heads, m.kv_heads, plan);
+  if (rc) return rc;
+  if ((rc = ensure_activations(c, T, B))) return rc;
+  if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
+
+  // One staged upload of every port (batch.go:385-405).
+  Stager sg;
+  const size_t o_ids = sg.add(s->ids, (size_t)T * 4);
+  const size_t o_posq = sg.add(s->posq, (size_t)T * m.heads * 4);
+  const size_t o_posk = sg.add(s->posk, (size_t)T * m.kv_heads * 4);
+  const size_t o_slots = sg.add(s->slots, (size_t)T * 4);
+  const size_t o_len = sg.add(s->lengths, (size_t)B * 4);
+  const size_t o_ext = sg.add(s->extents, (size_t)B * 4);
+  const size_t o_last = sg.add(s->last, (size_t)B * 4);
+  const size_t o_pages = sg.add(s->pages, (size_t)B * s->max_pages * 4);
+  const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
+  const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
+  const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  if ((rc = sg.upload(c))) return rc;
+  const hipStream_t st = c->stream;
+  TGOHIP_HIP(hipEventRecord(c->ev0, st));
+
+  const uint32_t* d_ids = sg.dev<uint32_t>(c, o_ids);
+  const uint32_t* d_ext = sg.dev<uint32_t>(c, o_ext);
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+                 sg.dev<uint32_t>(c, o_len), d_ext, sg.dev<uint32_t>(c, o_pages),
+                 (float*)c->part_o.p, (float*)c->part_ml.p};
+  const bool f32act = c->precision == 1;
+  const int actf16 = f32act ? 0 : 1;
+  const float scale = (float)(1.0 / std::sqrt((double)m.head_dim));  // session.go:821-823
+  float* h = (float*)c->h.p;
+  const size_t layer_kv = (size_t)c->kv_positions * m.kv_heads * kHeadDim;
+  float* ws = (float*)c->gemm_ws.p;
+  const size_t wsb = c->gemm_ws.bytes;
+
+  launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st);
+  for (int l = 0; l < m.layers; l++) {
+    const Layer& L = c->layers[l];
+    launch_rmsnorm(h, nullptr, T, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st);
+    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, T, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st))) return rc;
+    QKRopeArgs qa{(const float*)c->qkv.p, L.g_q, L.g_k, sg.dev<uint32_t>(c, o_posq),
+                  sg.dev<uint32_t>(c, o_posk), sg.dev<uint32_t>(c, o_slots), c->inv_freq,
+                  (float*)c->q.p, c->kc + l * layer_kv, c->vc + l * layer_kv, m.heads, m.kv_heads,
+                  c->kv_positions, m.rms_eps};
+    launch_qk_rope_kv(qa, T, st);
+    if ((rc = attn_enqueue(plan, dp, c->q.p, 0, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
+                           actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
+      return rc;
+    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st))) return rc;
+    launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st);
+    if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, T, c->act.p,
+                           f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
+      return rc;
+    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st))) return rc;
+  }
+  launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p, actf16, st);
+  if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
+    return rc;
+  launch_zero_idle((float*)c->logits.p, B, m.vocab, d_ext, st);
+  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st);
+  TGOHIP_HIP(hipEventRecord(c->ev1, st));
+  TGOHIP_HIP(hipGetLastError());
+  const auto t_sub = clk::now();
+  TGOHIP_HIP(hipEventSynchronize(c->ev1));
+  const auto t_dev = clk::now();
+  if (logits_out)
+    TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)B * m.vocab * 4, hipMemcpyDeviceToHost));
+  if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)B * 4, hipMemcpyDeviceToHost));
+  const auto t_end = clk::now();
+  if (tm) {
+    float dev_ms = 0;
+    (void)hipEventElapsedTime(&dev_ms, c->ev0, c->ev1);
+    tm->submit_ms = std::chrono::duration<double, std::milli>(t_sub - t_start).count();
+    tm->device_ms = dev_ms;
+    tm->readback_ms = std::chrono::duration<double, std::milli>(t_end - t_dev).count();
+  }
+  return 0;
+}
+
+// ---- op level ---------------------------------------------------------------
+int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int H, int H_kv,
+                           int head_dim, const void* k, const void* v, int capacity, int B,
+                           const uint32_t* lengths, const uint32_t* extents, const uint32_t* pages,
+                           int max_pages, int block, float scale, void* out, int out_dtype) {
+  if (head_dim != kHeadDim)
+    return fail(TGOHIP_EINVAL, "attention: head_dim is " + std::to_string(head_dim) +
+                                   "; the kernel is built for 128");
+  if (T < 0 || B < 0 || capacity <= 0) return fail(TGOHIP_EINVAL, "attention: T, B and capacity");
+  AttnPlan plan;
+  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan);
+  if (rc) return rc;
+  if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
+  Stager sg;
+  const size_t o_len = sg.add(lengths, (size_t)B * 4);
+  const size_t o_ext = sg.add(extents, (size_t)B * 4);
+  const size_t o_pages = sg.add(pages, (size_t)B * max_pages * 4);
+  const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
+  const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
+  const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  if ((rc = sg.upload(c))) return rc;
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+                 sg.dev<uint32_t>(c, o_len), sg.dev<uint32_t>(c, o_ext), sg.dev<uint32_t>(c, o_pages),
+                 (float*)c->part_o.p, (float*)c->part_ml.p};
+  return attn_enqueue(plan, dp, q, q_dtype == TGOHIP_F16, k, v, out, out_dtype == TGOHIP_F16, T, H,
+                      H_kv, max_pages, block, scale, c->stream);
+}
+
+// Plans once and replays the launch `iters` times (benchmark helper): the
+// metadata stays resident so each replay is the kernels alone.
+int tgohip_paged_attention_replay(tgohip_ctx* c, const void* q, int q_dtype, int T, int H, int H_kv,
+                                  const void* k, const void* v, int capacity, int B,
+                                  const uint32_t* lengths, const uint32_t* extents,
+                                  const uint32_t* pages, int max_pages, int block, float scale,
+                                  void* out, int out_dtype, int iters) {
+  AttnPlan plan;
+  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan);
+  if (rc) return rc;
+  if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
+  Stager sg;
+  const size_t o_len = sg.add(lengths, (size_t)B * 4);
+  const size_t o_ext = sg.add(extents, (size_t)B * 4);
+  const size_t o_pages = sg.add(pages, (size_t)B * max_pages * 4);
+  const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
+  const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
+  const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  if ((rc = sg.upload(c))) return rc;
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+                 sg.dev<uint32_t>(c, o_len), sg.dev<uint32_t>(c, o_ext), sg.dev<uint32_t>(c, o_pages),
+                 (float*)c->part_o.p, (float*)c->part_ml.p};
+  for (int i = 0; i < iters; i++)
+    if ((rc = attn_enqueue(plan, dp, q, q_dtype == TGOHIP_F16, k, v, out, out_dtype == TGOHIP_F16, T,
+                           H, H_kv, max_pages, block, scale, c->stream)))
+      return rc;
+  return 0;
+}
+
+int tgohip_weight_upload(tgohip_ctx* c, int form, int K, int N, const void* plane,
+                         const void* scales, const void* zeros, int* handle) {
+  int rc = check_shape(form, K, N, "weight");
+  if (rc) return rc;
+  Canon cn;
+  if ((rc = canon_upload(c, cn, form, K, N, plane, scales, zeros))) return rc;
+  PackedWeight w;
+  if ((rc = alloc_packed(c, w, form, K, N))) return rc;
+  if ((rc = repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, w, 1, 0, c->stream))) return rc;
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  *handle = c->next_handle++;
+  c->handles[*handle] = w;
+  return 0;
+}
+
+// Synthesises a weight on the device under a handle (benchmark shapes).
+int tgohip_weight_synth(tgohip_ctx* c, int form, int K, int N, uint64_t seed, uint64_t stream,
+                        double sigma, int* handle) {
+  int rc = check_shape(form, K, N, "weight");
+  if (rc) return rc;
+  Canon cn;
+  if ((rc = canon_synth(c, cn, seed, stream, form, K, N, sigma))) return rc;
+  PackedWeight w;
+  if ((rc = alloc_packed(c, w, form, K, N))) return rc;
+  if ((rc = repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, w, 1, 0, c->stream))) return rc;
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  *handle = c->next_handle++;
+  c->handles[*handle] = w;
+  return 0;
+}
+
+int tgohip_weight_free(tgohip_ctx* c, int handle) {
+  auto it = c->handles.find(handle);
+  if (it == c->handles.end()) return fail(TGOHIP_EINVAL, "weight_free: no handle " + std::to_string(handle));
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  free_packed(c, it->second);
+  c->handles.erase(it);
+  return 0;
+}
+
+static PackedWeight* handle_of(tgohip_ctx* c, int handle) {
+  auto it = c->handles.find(handle);
+  if (it == c->handles.end()) {
+    fail(TGOHIP_EINVAL, "no weight handle " + std::to_string(handle));
+    return nullptr;
+  }
+  return &it->second;
+}
+
+int tgohip_linear(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, void* y, int y_dtype) {
+  PackedWeight* w = handle_of(c, handle);
+  if (!w) return TGOHIP_EINVAL;
+  const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
+  int rc = c->gemm_ws.ensure(ws + 256);
+  if (rc) return rc;
+  return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
+                      (float*)c->gemm_ws.p, c->gemm_ws.bytes, c->ncu, c->stream);
+}
+
+int tgohip_dequant(tgohip_ctx* c, int handle, float* y) {
+  PackedWeight* w = handle_of(c, handle);
+  if (!w) return TGOHIP_EINVAL;
+  return dequant_enqueue(*w, y, false, c->stream);
+}
+
+int tgohip_dequant_f16(tgohip_ctx* c, int handle, uint16_t* y) {
+  PackedWeight* w = handle_of(c, handle);
+  if (!w) return TGOHIP_EINVAL;
+  return dequant_enqueue(*w, y, true, c->stream);
+}
+
+}  // extern "C"
+
+// ===========================================================================
+// Scheduler: scheduler.go + Batch (batch.go) over the prefix pool
+// ===========================================================================
+struct SchedSlot {
+  bool live = false;
+  std::vector<int32_t> prompt;
+  int prefilled = 0;
+  int feed = 0;
+  int reused = 0;
+  uint64_t arrived = 0;
+  PrefixLease* lease = nullptr;
+  std::vector<int> pages;
+  int length = 0;
+};
+
+struct tgohip_sched {
+  tgohip_ctx* ctx;
+  int chunk, reserve, max_rows;
+  std::unique_ptr<PrefixPool> pool;
+  std::vector<SchedSlot> slots;
+  uint64_t next = 0;
+  // reusable host buffers
+  std::vector<uint32_t> ids, posq, posk, slotv, lengths, extents, last, table;
+  std::vector<int32_t> argmax;
+};
+
+static void slot_release(SchedSlot& s) {
+  if (s.lease) {
+    s.lease->release();
+    delete s.lease;
+    s.lease = nullptr;
+  }
+  s.pages.clear();
+}
+
+extern "C" {
+
+tgohip_sched* tgohip_sched_new(tgohip_ctx* c, int n, int chunk, int reserve, int max_rows) {
+  if (reserve <= 0) {
+    fail(TGOHIP_EINVAL, "the scheduler's reserve is " + std::to_string(reserve) +
+                            "; it is how many positions an admitted sequence may grow by, and "
+                            "admitting without one fills every slot with sequences that cannot grow");
+    return nullptr;
+  }
+  if (chunk == 0) chunk = 512;  // DefaultChunk (schedule.go:21)
+  if (chunk < 0) {
+    fail(TGOHIP_EINVAL, "the prefill chunk is " + std::to_string(chunk) + "; a chunk is at least one token");
+    return nullptr;
+  }
+  if (n < 2) {
+    fail(TGOHIP_EINVAL, "a batch of " + std::to_string(n) + " slot(s) is a session; a batch is two or more");
+    return nullptr;
+  }
+  if (!c->kc) {
+    fail(TGOHIP_ESTATE, "a batched step needs a shared block pool");
+    return nullptr;
+  }
+  auto* s = new tgohip_sched();
+  s->ctx = c;
+  s->chunk = chunk;
+  s->reserve = reserve;
+  s->max_rows = max_rows > 0 ? max_rows : c->kv_positions;
+  s->pool.reset(new PrefixPool(c->cfg.block, c->kv_positions / c->cfg.block, 0));
+  s->slots.resize(n);
+  return s;
+}
+
+void tgohip_sched_free(tgohip_sched* s) {
+  if (!s) return;
+  for (auto& sl : s->slots) slot_release(sl);
+  delete s;
+}
+
+int tgohip_sched_admit(tgohip_sched* s, const int32_t* prompt, int n, int reserve) {
+  if (reserve == 0) reserve = s->reserve;
+  if (reserve < 0) return fail(TGOHIP_EINVAL, "the reserve is " + std::to_string(reserve));
+  if (n <= 0) return fail(TGOHIP_EINVAL, "the prompt is empty; there is nothing to condition on");
+  int free = -1;
+  for (int i = 0; i < (int)s->slots.size(); i++)
+    if (!s->slots[i].live) { free = i; break; }
+  if (free < 0) return fail(TGOHIP_ENOSLOT, "every slot is occupied");
+  SchedSlot& sl = s->slots[free];
+  slot_release(sl);
+  PrefixLease* l = nullptr;
+  int rc = s->pool->acquire(prompt, n, "", "", reserve, &l);
+  if (rc) return rc;
+  sl.lease = l;
+  sl.pages = l->blocks;
+  sl.length = l->reused;
+  s->next++;
+  sl.live = true;
+  sl.prompt.assign(prompt, prompt + n);
+  sl.prefilled = l->reused;
+  sl.reused = l->reused;
+  sl.arrived = s->next;
+  sl.feed = 0;
+  return free;
+}
+
+int tgohip_sched_finish(tgohip_sched* s, int slot) {
+  if (slot < 0 || slot >= (int)s->slots.size())
+    return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " is outside a batch of " +
+                                   std::to_string(s->slots.size()));
+  SchedSlot& sl = s->slots[slot];
+  slot_release(sl);
+  sl = SchedSlot();
+  return 0;
+}
+
+int tgohip_sched_evict(tgohip_sched* s) {
+  std::vector<int32_t> live, plen, pf;
+  std::vector<uint64_t> arr;
+  for (auto& sl : s->slots) {
+    live.push_back(sl.live);
+    plen.push_back((int32_t)sl.prompt.size());
+    pf.push_back(sl.prefilled);
+    arr.push_back(sl.arrived);
+  }
+  const int v = tgohip_victim((int)s->slots.size(), live.data(), plen.data(), pf.data(), arr.data());
+  if (v < 0) return -1;
+  tgohip_sched_finish(s, v);
+  return v;
+}
+
+int tgohip_sched_feed(tgohip_sched* s, int slot, int token) {
+  if (slot < 0 || slot >= (int)s->slots.size())
+    return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " is outside a batch of " +
+                                   std::to_string(s->slots.size()));
+  SchedSlot& sl = s->slots[slot];
+  if (!sl.live) return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " holds no sequence");
+  if (sl.prefilled < (int)sl.prompt.size())
+    return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " is " + std::to_string(sl.prefilled) +
+                                   " tokens into a " + std::to_string(sl.prompt.size()) +
+                                   "-token prompt; a token fed before the prompt is scored would be "
+                                   "generated from a distribution over the middle of it");
+  if (token < 0 || token >= s->ctx->cfg.vocab)
+    return fail(TGOHIP_EINVAL, "token id " + std::to_string(token) +
+                                   " is outside the model's vocabulary of " + std::to_string(s->ctx->cfg.vocab));
+  sl.feed = token;
+  sl.prompt.push_back(token);
+  sl.prefilled++;
+  return 0;
+}
+
+int tgohip_sched_length(tgohip_sched* s, int slot) {
+  if (slot < 0 || slot >= (int)s->slots.size()) return 0;
+  return s->slots[slot].length;
+}
+
+int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, int32_t* out_done,
+                      int32_t* prefill_tokens, int32_t* decodes, tgohip_timings* tm) {
+  const int n = (int)s->slots.size();
+  const tgohip_model_cfg& m = s->ctx->cfg;
+  std::vector<int32_t> live(n), plen(n), pf(n), ws(n), wst(n), wc(n);
+  for (int i = 0; i < n; i++) {
+    live[i] = s->slots[i].live;
+    plen[i] = (int32_t)s->slots[i].prompt.size();
+    pf[i] = s->slots[i].prefilled;
+  }
+  int32_t nw = 0, npf = 0, ndc = 0;
+  int rc = tgohip_next_step(n, live.data(), plen.data(), pf.data(), s->chunk, s->max_rows, ws.data(),
+                            wst.data(), wc.data(), &nw, &npf, &ndc);
+  if (rc) return rc;
+  *prefill_tokens = npf;
+  *decodes = ndc;
+  if (nw == 0) return 0;
+  // Batch.step: every slot is a member; workers reserve blocks first.
+  std::vector<int32_t> counts(n, 0), first(n, 0), toks;
+  std::vector<std::vector<int32_t>> wtok(n);
+  for (int i = 0; i < nw; i++) {
+    const int sl = ws[i];
+    SchedSlot& st = s->slots[sl];
+    if (wst[i] >= 0) wtok[sl].assign(st.prompt.begin() + wst[i], st.prompt.begin() + wst[i] + wc[i]);
+    else wtok[sl] = {st.feed};
+    const int need = st.length + (int)wtok[sl].size();
+    if (need > (int)st.lease->ids.size()) {
+      if ((rc = st.lease->grow(need - (int)st.lease->ids.size()))) return rc;
+    }
+    st.pages = st.lease->blocks;
+  }
+  int total = 0, maxp = 1;
+  for (int i = 0; i < n; i++) {
+    first[i] = s->slots[i].length;
+    counts[i] = (int32_t)wtok[i].size();
+    total += counts[i];
+    maxp = std::max(maxp, (int)s->slots[i].pages.size());
+    toks.insert(toks.end(), wtok[i].begin(), wtok[i].end());
+  }
+  const int maxPages = s->ctx->kv_positions / m.block;
+  std::vector<int32_t> pagesv((size_t)n * maxPages, 0), plens(n, 0);
+  s->table.assign((size_t)n * maxPages, 0u);
+  for (int i = 0; i < n; i++) {
+    plens[i] = (int32_t)s->slots[i].pages.size();
+    for (size_t j = 0; j < s->slots[i].pages.size(); j++) {
+      pagesv[(size_t)i * maxPages + j] = s->slots[i].pages[j];
+      s->table[(size_t)i * maxPages + j] = (uint32_t)s->slots[i].pages[j];
+    }
+  }
+  const int rows = total;
+  s->ids.resize(rows);
+  s->posq.resize((size_t)rows * m.heads);
+  s->posk.resize((size_t)rows * m.kv_heads);
+  s->slotv.resize(rows);
+  s->lengths.resize(n);
+  s->extents.resize(n);
+  s->last.resize(n);
+  s->argmax.resize(n);
+  rc = tgohip_new_batch_step(m.vocab, m.heads, m.kv_heads, rows, n, toks.data(), counts.data(),
+                             first.data(), pagesv.data(), plens.data(), maxPages, m.block,
+                             s->ctx->kv_positions, s->ids.data(), s->posq.data(), s->posk.data(),
+                             s->slotv.data(), s->lengths.data(), s->extents.data(), s->last.data());
+  if (rc) return rc;
+  tgohip_batch_step bs{rows, n, maxPages, s->ids.data(), s->posq.data(), s->posk.data(),
+                       s->slotv.data(), s->lengths.data(), s->extents.data(), s->last.data(),
+                       s->table.data()};
+  if ((rc = tgohip_step(s->ctx, &bs, nullptr, s->argmax.data(), tm))) return rc;
+  // commit: the step landed (batch.go:443-456), then the scheduler's books.
+  int produced = 0;
+  for (int i = 0; i < nw; i++) {
+    const int sl = ws[i];
+    SchedSlot& st = s->slots[sl];
+    const std::vector<int32_t>& tk = wtok[sl];
+    const int need = st.length + (int)tk.size();
+    if (need > (int)st.lease->ids.size()) {
+      const int extra = need - (int)st.lease->ids.size();
+      if ((rc = st.lease->commit(tk.data() + tk.size() - extra, extra))) return rc;
+    }
+    st.lease->publish(st.length + (int)tk.size());
+    st.pages = st.lease->blocks;
+    st.length += (int)tk.size();
+    const bool prefill = st.prefilled < (int)st.prompt.size();
+    if (prefill) st.prefilled += (int)tk.size();
+    out_slot[produced] = sl;
+    out_token[produced] = s->argmax[sl];
+    out_done[produced] = st.prefilled >= (int)st.prompt.size();
+    produced++;
+  }
+  return produced;
+}
+
+}  // extern "C"
