@@ -178,7 +178,7 @@ def chain(prev, ids):
     h = hashlib.sha256()
     h.update(prev)
     for i in ids:
-        h.update(struct.pack("<Q", i & 0xFFFFFFFFFFFFFFFF))
+        h.update(struct.pack("<Q", int(i) & 0xFFFFFFFFFFFFFFFF))
     return h.digest()
 
 

@@ -113,7 +113,16 @@ uint16_t orc_f32_to_f16_bits(float x, int* saturated) {
   return (uint16_t)(sign | (uint16_t)(((uint32_t)(e + 15) << 10) + round_shift(mant, 13)));
 }
 
-float orc_f16_to_f32(uint16_t h) {
+static float f16_table[65536];
+static float f16_to_f32_slow(uint16_t h);
+/* Every f16 bit pattern widened once at load; widening is exact, so the
+ * table is the same function as f16_to_f32_slow. */
+__attribute__((constructor)) static void init_f16_table(void) {
+  for (uint32_t i = 0; i < 65536; i++) f16_table[i] = f16_to_f32_slow((uint16_t)i);
+}
+float orc_f16_to_f32(uint16_t h) { return f16_table[h]; }
+
+static float f16_to_f32_slow(uint16_t h) {
   uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
   if (e == 0) {
     if (m == 0) return bitsf32(sign);

@@ -1,0 +1,255 @@
+"""Whole batched steps on the GPU against tgo's CPU path restated (oracle.c).
+
+The step is driven like Batch.step (batch.go:314-458): every slot is a
+member, the packing is model.NewBatchStep's (restated in oracle/host.py),
+pages come from a prefix pool, and the same ports go to the GPU
+(tgohip_step) and to the CPU restatement (orc_model_step).
+
+Budgets, written here:
+  * logits: |gpu - cpu| <= 2e-3 * max|cpu| per row (BASELINE's 2e-3 relative
+    bound, scaled by the row's magnitude);
+  * greedy ids (first strict maximum, sample/stages.go:196-206) identical
+    for every step, the C1 config's 64-step requirement;
+  * batched vs apart (batch_test.go:72-200): 1e-5 relative + same argmax.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import host
+
+pytestmark = pytest.mark.gpu
+
+
+class Engine:
+    """Batch.step's host half over a backend that runs the forward pass."""
+
+    def __init__(self, backend, vocab, heads, kv_heads, positions, block, nslots):
+        self.backend = backend
+        self.V, self.H, self.Hkv, self.block = vocab, heads, kv_heads, block
+        self.capacity = positions
+        self.max_pages = positions // block
+        self.pool = host.Pool(block, positions // block)
+        self.slots = [dict(lease=None, length=0) for _ in range(nslots)]
+
+    def admit(self, slot, prompt, reserve):
+        lease = self.pool.acquire(prompt, reserve=reserve)
+        self.slots[slot] = dict(lease=lease, length=lease.reused)
+
+    def step(self, work):
+        members = [host.Member([], s["length"], list(s["lease"].blocks) if s["lease"] else [])
+                   for s in self.slots]
+        for slot, toks in work:
+            s = self.slots[slot]
+            need = s["length"] + len(toks)
+            if need > len(s["lease"].ids):
+                s["lease"].grow(need - len(s["lease"].ids))
+            members[slot] = host.Member(list(toks), s["length"], list(s["lease"].blocks))
+        rows = sum(len(t) for _, t in work)
+        st = host.new_batch_step(self.V, self.H, self.Hkv, rows, members, self.block,
+                                 self.capacity)
+        table = host.page_table([m.pages for m in members], self.max_pages)
+        logits = self.backend(st, table, self.max_pages)
+        for slot, toks in work:
+            s = self.slots[slot]
+            need = s["length"] + len(toks)
+            if need > len(s["lease"].ids):
+                extra = need - len(s["lease"].ids)
+                s["lease"].commit(list(toks[len(toks) - extra:]))
+            s["lease"].publish(s["length"] + len(toks))
+            s["length"] += len(toks)
+        return logits
+
+
+def gpu_backend(ctx):
+    def run(st, table, max_pages):
+        logits, _, _ = ctx.step(st, table, max_pages, want_argmax=False)
+        return logits
+    return run
+
+
+def cpu_backend(model):
+    def run(st, table, max_pages):
+        return model.step(st, table, max_pages)
+    return run
+
+
+def argmax_first(row):
+    return int(np.argmax(row))  # numpy returns the first maximal index
+
+
+def top2_margin(row):
+    s = np.sort(row)
+    return float(s[-1] - s[-2])
+
+
+def check_logits(gpu, cpu, rows, what):
+    for r in rows:
+        bound = 2e-3 * np.abs(cpu[r]).max()
+        err = np.abs(gpu[r] - cpu[r]).max()
+        assert err <= bound, (what, r, err, bound)
+
+
+SMALL = dict(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1024,
+             eps=1e-6, theta=1e6, block=4, positions=256)
+
+
+def make_pair(torch, cfg, form, seed, precision):
+    import tgo_amd
+    ctx = tgo_amd.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    ctx.set_precision(precision)
+    ctx.config(cfg["layers"], cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
+               cfg["ffn"], cfg["vocab"], cfg["eps"], cfg["theta"], cfg["block"])
+    ctx.synth_weights(seed, form, 0.02)
+    ctx.kv_alloc(cfg["positions"])
+    cpu = oracle.CPUModel(cfg["layers"], cfg["hidden"], cfg["heads"], cfg["kv_heads"],
+                          cfg["head_dim"], cfg["ffn"], cfg["vocab"], cfg["eps"], cfg["theta"],
+                          cfg["block"], cfg["positions"])
+    cpu.synth(seed, form, 0.02)
+    return ctx, cpu
+
+
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+@pytest.mark.parametrize("precision", [0, 1])
+def test_mixed_step_matches_the_cpu_path(torch_gpu, form, precision):
+    """batch_test.go:72-200's shape: a chunk of 3, a decode, an empty slot, scattered pages."""
+    cfg = SMALL
+    ctx, cpu = make_pair(torch_gpu, cfg, form, 11 + form, precision)
+    try:
+        engines = [Engine(b, cfg["vocab"], cfg["heads"], cfg["kv_heads"], cfg["positions"],
+                          cfg["block"], 3) for b in (gpu_backend(ctx), cpu_backend(cpu))]
+        rng = np.random.default_rng(form)
+        p0 = [int(t) for t in rng.integers(0, cfg["vocab"], 7)]
+        p1 = [int(t) for t in rng.integers(0, cfg["vocab"], 5)]
+        for e in engines:
+            e.admit(0, p0, 4)
+            e.admit(1, p1, 4)
+        # prefill both, then the mixed step: a chunk of 3 for a new slot plus one decode
+        outs = [e.step([(0, p0), (1, p1)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1], "prefill")
+        p2 = [int(t) for t in rng.integers(0, cfg["vocab"], 3)]
+        for e in engines:
+            e.admit(2, p2, 4)
+        t0 = argmax_first(outs[1][0])
+        outs = [e.step([(0, [t0]), (2, p2)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 2], "mixed")
+        assert np.all(outs[0][1] == 0)  # the slot with nothing to say
+    finally:
+        ctx.close()
+        cpu.close()
+
+
+def test_batched_step_equals_the_steps_apart(torch_gpu):
+    """batch_test.go:72-200: 1e-5 relative and the same argmax, per sequence."""
+    cfg = SMALL
+    import tgo_amd
+    ctx, cpu = make_pair(torch_gpu, cfg, 3, 5, 1)
+    try:
+        rng = np.random.default_rng(1)
+        prompts = [list(rng.integers(0, cfg["vocab"], n)) for n in (6, 9)]
+        e = Engine(gpu_backend(ctx), cfg["vocab"], cfg["heads"], cfg["kv_heads"],
+                   cfg["positions"], cfg["block"], 2)
+        for i, p in enumerate(prompts):
+            e.admit(i, p, 4)
+        together = e.step([(0, prompts[0]), (1, prompts[1])])
+        # the same two prefills apart (the cache is rewritten identically)
+        e2 = Engine(gpu_backend(ctx), cfg["vocab"], cfg["heads"], cfg["kv_heads"],
+                    cfg["positions"], cfg["block"], 2)
+        for i, p in enumerate(prompts):
+            e2.admit(i, p, 4)
+        a0 = e2.step([(0, prompts[0])])
+        a1 = e2.step([(1, prompts[1])])
+        for s, apart in ((0, a0), (1, a1)):
+            rel = np.abs(together[s] - apart[s]).max() / np.abs(apart[s]).max()
+            assert rel <= 1e-5, (s, rel)
+            assert argmax_first(together[s]) == argmax_first(apart[s])
+    finally:
+        ctx.close()
+        cpu.close()
+
+
+def test_kv_rows_are_the_cast_projections(torch_gpu):
+    """nn/attention.go:225-232: K (normed, rotated) and V rows land at slots[t] as f16,
+    pad rows (slot = capacity) write nothing."""
+    cfg = SMALL
+    ctx, cpu = make_pair(torch_gpu, cfg, 0, 3, 1)
+    try:
+        rng = np.random.default_rng(4)
+        e_g = Engine(gpu_backend(ctx), cfg["vocab"], cfg["heads"], cfg["kv_heads"],
+                     cfg["positions"], cfg["block"], 2)
+        e_c = Engine(cpu_backend(cpu), cfg["vocab"], cfg["heads"], cfg["kv_heads"],
+                     cfg["positions"], cfg["block"], 2)
+        p = [int(t) for t in rng.integers(0, cfg["vocab"], 10)]
+        for e in (e_g, e_c):
+            e.admit(0, p, 2)
+            e.step([(0, p)])
+        torch = torch_gpu
+        kp, vp, npos = ctx.kv_pointers()
+        n = cfg["layers"] * npos * cfg["kv_heads"] * 128
+        dk = torch.empty(n, dtype=torch.int16, device="cuda")
+        dv = torch.empty(n, dtype=torch.int16, device="cuda")
+        import ctypes
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        torch.cuda.synchronize()
+        assert hip.hipMemcpy(ctypes.c_void_p(dk.data_ptr()), ctypes.c_void_p(kp), n * 2, 3) == 0
+        assert hip.hipMemcpy(ctypes.c_void_p(dv.data_ptr()), ctypes.c_void_p(vp), n * 2, 3) == 0
+        gk = dk.cpu().numpy().view(np.uint16).astype(np.uint16)
+        gv = dv.cpu().numpy().view(np.uint16).astype(np.uint16)
+        ck, cv = cpu.kv()
+        gkf = gk.view(np.float16).astype(np.float32)
+        ckf = ck.view(np.float16).astype(np.float32)
+        gvf = gv.view(np.float16).astype(np.float32)
+        cvf = cv.view(np.float16).astype(np.float32)
+        # rows not written are still zero on both sides
+        assert np.array_equal(gk == 0, ck == 0) or np.abs(gkf - ckf).max() < 1e-2
+        assert np.abs(gkf - ckf).max() <= 2e-3 * np.abs(ckf).max() + 2.0 ** -10
+        assert np.abs(gvf - cvf).max() <= 2e-3 * np.abs(cvf).max() + 2.0 ** -10
+        assert np.abs(ckf).max() > 0
+    finally:
+        ctx.close()
+        cpu.close()
+
+
+C1 = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, ffn=3072, vocab=151936,
+          eps=1e-6, theta=1e6, block=16, positions=4096)
+
+
+@pytest.mark.parametrize("precision", [1, 0])
+def test_c1_step_and_64_greedy_steps(torch_gpu, precision):
+    """Qwen3-0.6B-shaped, f16 weights N(0,0.02) from a seed; 3 decode
+    sequences with contexts {37,300,511} plus a 64-token chunk on a fresh sequence, page 16;
+    then 64 greedy steps. Logits within 2e-3 of the CPU path, greedy ids identical."""
+    cfg = C1
+    ctx, cpu = make_pair(torch_gpu, cfg, 0, 2026, precision)
+    try:
+        V = cfg["vocab"]
+        rng = np.random.default_rng(7)
+        prompts = [list(rng.integers(0, V, n)) for n in (37, 300, 511)]
+        fresh = [int(t) for t in rng.integers(0, V, 64)]
+        engines = [Engine(b, V, cfg["heads"], cfg["kv_heads"], cfg["positions"], cfg["block"], 4)
+                   for b in (gpu_backend(ctx), cpu_backend(cpu))]
+        for e in engines:
+            for i, p in enumerate(prompts):
+                e.admit(i, p, 80)
+        outs = [e.step([(i, p) for i, p in enumerate(prompts)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1, 2], "contexts")
+        toks = [[argmax_first(o[i]) for i in range(3)] for o in outs]
+        assert toks[0] == toks[1]
+        for e in engines:
+            e.admit(3, fresh, 80)
+        margins = []
+        work = [(i, [toks[1][i]]) for i in range(3)] + [(3, fresh)]
+        for step in range(65):
+            outs = [e.step(work) for e in engines]
+            check_logits(outs[0], outs[1], range(4), "step %d" % step)
+            g = [argmax_first(outs[0][i]) for i in range(4)]
+            c = [argmax_first(outs[1][i]) for i in range(4)]
+            margins.append(min(top2_margin(outs[1][i]) for i in range(4)))
+            assert g == c, ("greedy diverged", step, g, c, margins[-1])
+            work = [(i, [c[i]]) for i in range(4)]
+        print("C1 precision %d: min top-2 margin over 65 steps %.3g" % (precision, min(margins)))
+    finally:
+        ctx.close()
+        cpu.close()
