@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""bench.py -- the headline benchmark: BASELINE config 4 on one MI355X.
+
+Workload (config 4): a Qwen3-8B-shaped decoder (36 layers, hidden 4096,
+32 q / 8 kv heads, head_dim 128, MLP 12288, vocab 151936) with random-init
+int4 weights (the BASELINE pack: symmetric, group 32 along K, f16 scales; the
+embedding int8), continuous batching through the library's Scheduler
+(scheduler.go semantics, chunk 512): 128 decoding sequences whose contexts are
+lognormal(median 1024, sigma 1.0) clipped to [16, 8192] tokens, plus 2 prefill
+chunks of 512 tokens per step, page size 16, f16 KV pool, greedy sampling on
+the device. Arrivals and completions are seeded: each request has a prompt of
+the same lognormal length and an output budget U[100, 300]; a finished
+sequence frees its slot and the next arrival is admitted when fewer than two
+requests are mid-prefill. The initial 128 decoders are admitted with their
+context already in the pool (synthetic KV), so step 1 is already steady state.
+
+A step is one Scheduler.Step: one batched forward pass over ~1152 rows.
+value = output tokens (sampleable tokens produced) / wall time of the timed
+steps, inputs resident in HBM. The roofline object is the ragged paged
+attention kernel (the metric's "paged-attn HBM GB/s"): algorithmic bytes per
+launch (every cached position a claimed row reads, K+V of the 8 kv heads
+once = 4096 B per position, plus 24 KiB per query row for q in and out)
+divided by its duration, bracketed with HIP events on the launch stream over
+the timed steps. cpu_baseline times tgo's CPU path restated (oracle/) on one
+of the timed steps: the step with 1 and with 2 layers, extrapolated to 36.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+C4 = dict(layers=36, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=151936,
+          rms_eps=1e-6, rope_theta=1e6, block=16)
+SEED = 2026
+POOL = 400_000          # positions in the shared KV pool (59 GB of f16 K+V)
+SLOTS = 136             # 128 decoders + 2 prefilling + headroom
+CHUNK = 512
+DECODERS = 128
+PREFILLING = 2
+HBM_PEAK = 8000.0       # GB/s, MI355X published
+MFMA_F16_PEAK = 2500.0  # TFLOP/s dense f16, MI355X published
+
+
+def lognormal_len(rng):
+    return int(min(8192, max(16, round(math.exp(math.log(1024) + 1.0 * rng.standard_normal())))))
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--precision", type=int, default=0,
+                   help="0: f16 activations into the MFMA (default); 1: f32 activations (hi+lo)")
+    p.add_argument("--form", type=int, default=3, help="weight form (3: int4 sym g32-K, 2: tgo int4)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+class Workload:
+    """Seeded arrivals and completions driving the library's Scheduler so that
+    every step carries 128 decodes and 2 prefill chunks of 512.
+
+    Arrival prompts are lognormal(median 1024, sigma 1) clipped to [16, 8192]
+    and rounded up to whole chunks, so each chunk is exactly 512 tokens. When a
+    request finishes its prompt it starts decoding, and the decoder closest to
+    its output budget (U[100,300], seeded) completes, freeing its slot for the
+    next arrival: 128 decoders and 2 prefilling requests at every step."""
+
+    def __init__(self, tgo, ctx, seed):
+        self.rng = np.random.default_rng(seed)
+        self.sched = tgo.Scheduler(ctx, SLOTS, chunk=CHUNK, reserve=512,
+                                   max_rows=PREFILLING * CHUNK + DECODERS)
+        self.target = {}
+        self.made = {}
+        self.decoding = set()
+        self.V = C4["vocab"]
+        used = 0
+        for _ in range(DECODERS):
+            L = lognormal_len(self.rng)
+            out = int(self.rng.integers(100, 301))
+            prompt = [int(t) for t in self.rng.integers(0, self.V, L)]
+            slot = self.sched.admit_prefilled(prompt, int(self.rng.integers(0, self.V)),
+                                              reserve=out)
+            # already part-way through its answer: completions are spread from step 1
+            self.target[slot], self.made[slot] = out, int(self.rng.integers(0, out))
+            self.decoding.add(slot)
+            used += L + out
+        self.used_positions = used
+        self.contexts = [self.sched.length(s) for s in sorted(self.decoding)]
+        self.admit_arrivals()
+
+    def admit_arrivals(self):
+        while self.sched.prefilling() < PREFILLING:
+            L = CHUNK * ((lognormal_len(self.rng) + CHUNK - 1) // CHUNK)
+            out = int(self.rng.integers(100, 301))
+            prompt = [int(t) for t in self.rng.integers(0, self.V, L)]
+            slot = self.sched.admit(prompt, reserve=out)
+            self.target[slot], self.made[slot] = out, 0
+
+    def step(self):
+        produced, prefill, decodes, tm = self.sched.step()
+        out = 0
+        started = 0
+        for slot, tok, done in produced:
+            if not done:
+                continue
+            out += 1
+            self.made[slot] += 1
+            if slot not in self.decoding:
+                self.decoding.add(slot)
+                started += 1
+            self.sched.feed(slot, tok)
+        # each request that started decoding retires the decoder nearest its budget
+        for _ in range(started):
+            slot = max(self.decoding, key=lambda s: (self.made[s] / self.target[s], -s))
+            self.decoding.discard(slot)
+            self.sched.finish(slot)
+        self.admit_arrivals()
+        return out, prefill, decodes, tm
+
+
+def cpu_baseline(st, pages, max_pages, out_tokens, form):
+    """tgo's CPU path restated (oracle/, OpenMP) on one timed step: the step with 1
+    and 2 layers, the per-layer time extrapolated to 36 layers."""
+    import oracle
+    c = C4
+    m = oracle.CPUModel(2, c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"],
+                        c["vocab"], c["rms_eps"], c["rope_theta"], c["block"], POOL)
+    try:
+        m.synth(SEED, form, 0.02, 2)
+        t = time.perf_counter()
+        m.step(st, pages, max_pages, layers=1)
+        t1 = time.perf_counter() - t
+        t = time.perf_counter()
+        m.step(st, pages, max_pages, layers=2)
+        t2 = time.perf_counter() - t
+    finally:
+        m.close()
+    per_layer = max(t2 - t1, 1e-9)
+    full = t1 + (c["layers"] - 1) * per_layer
+    return dict(value=out_tokens / full, unit="tok/s", cores=int(oracle.lib.orc_num_threads()),
+                kind="port",
+                sample=("one timed step (%d rows, %d sequences) of the same workload run by the "
+                        "CPU restatement with 1 layer (%.1f s) and 2 layers (%.1f s); step time "
+                        "extrapolated to 36 layers = %.1f s; KV contents zero, weights the same "
+                        "synthesized int4" % (len(st["ids"]), len(st["lengths"]), t1, t2, full)),
+                seconds=t1 + t2)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build measures one MI355X; --gpus %d is not supported (the path "
+              "would shard attention by sequence and the projections by column/row with RCCL, "
+              "see DESIGN.md)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    import tgo_amd
+    t_setup = time.perf_counter()
+    ctx = tgo_amd.Context(0)
+    ctx.set_precision(args.precision)
+    ctx.config(C4["layers"], C4["hidden"], C4["heads"], C4["kv_heads"], C4["head_dim"],
+               C4["ffn"], C4["vocab"], C4["rms_eps"], C4["rope_theta"], C4["block"])
+    ctx.synth_weights(SEED, args.form, 0.02)
+    ctx.kv_alloc(POOL)
+    wl = Workload(tgo_amd, ctx, SEED)
+    ctx.kv_synth(SEED, 1.0, min(POOL, wl.used_positions + 64 * CHUNK))
+    setup_s = time.perf_counter() - t_setup
+    print("setup %.1f s: weights synthesized, %d decoders admitted (mean context %.0f)" %
+          (setup_s, DECODERS, np.mean([x for x in wl.contexts if x > 0])), file=sys.stderr,
+          flush=True)
+
+    for i in range(args.warmup):
+        wl.step()
+    ctx.sync()
+    ctx.set_profile(True)
+    total_out = total_pf = total_dc = 0
+    dev_ms = 0.0
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        out, pf, dc, tm = wl.step()
+        total_out += out
+        total_pf += pf
+        total_dc += dc
+        dev_ms += tm.device_ms
+        if (i + 1) % 50 == 0:
+            print("step %d/%d: %.1f ms/step so far" % (i + 1, args.steps,
+                  1e3 * (time.perf_counter() - t0) / (i + 1)), file=sys.stderr, flush=True)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    attn_ms, attn_bytes, launches = ctx.profile_read()
+    ctx.set_profile(False)
+    last_st, last_pages, maxp = wl.sched.last_step()
+    # the CPU leg is charged the mean output tokens of a timed step
+    last_out = total_out / args.steps
+
+    avg_attn_ms = attn_ms / max(launches, 1)
+    achieved = (attn_bytes / max(launches, 1)) / (avg_attn_ms * 1e-3) / 1e9
+    rows_per_step = (total_pf + total_dc) / args.steps
+    result = {
+        "metric": "output tok/s, Qwen3-8B int4 ragged batch, 1 MI355X; paged-attn HBM GB/s",
+        "value": round(total_out / elapsed, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * elapsed / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.precision == 0 else "f16x2 (f32 activations)",
+        "data": "synthetic (seeded random-init int4 weights, seeded token ids, synthetic KV for "
+                "the initial contexts)",
+        "config": {
+            "workload": "BASELINE config 4: Qwen3-8B-shaped int4 (symmetric g32-K pack), 128 "
+                        "decode sequences (contexts lognormal median 1024, sigma 1.0, clipped "
+                        "[16,8192]) + 2 prefill chunks of 512 per step, page 16, f16 KV, greedy, "
+                        "seeded arrivals/completions",
+            "weight_form": {3: "int4-sym-g32K", 2: "int4-tgo-g128-asym", 1: "int8", 0: "f16"}[args.form],
+            "rows_per_step": round(rows_per_step, 1),
+            "prefill_tokens_per_step": round(total_pf / args.steps, 1),
+            "decodes_per_step": round(total_dc / args.steps, 1),
+            "output_tokens": int(total_out),
+            "device_ms_per_step": round(dev_ms / args.steps, 3),
+        },
+        "roofline": {
+            "kernel": "attn_kernel + attn_combine_kernel (ragged paged attention)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": None,
+            "avg_launch_ms": round(avg_attn_ms, 4),
+            "algorithmic_bytes_per_launch": round(attn_bytes / max(launches, 1)),
+            "launches": launches,
+        },
+        "cpu_baseline": None,
+    }
+    ctx.close()
+    if not args.no_cpu:
+        cb = cpu_baseline(last_st, last_pages, maxp, last_out, args.form)
+        cb.pop("seconds")
+        result["cpu_baseline"] = cb
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

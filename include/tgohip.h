@@ -257,6 +257,31 @@ int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
                       int32_t* out_done, int32_t* prefill_tokens, int32_t* decodes,
                       tgohip_timings* t);
 
+/* Admits a sequence whose prompt's KV is already resident (restored, or
+ * synthetic in a benchmark): the slot starts decoding with token `feed`. */
+int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, int reserve,
+                                 int feed);
+int tgohip_sched_prefilling(tgohip_sched* s); /* live slots still mid-prefill */
+int tgohip_sched_live(tgohip_sched* s);       /* live slots */
+/* The ports of the last step (Batch.step's packing): sizes first with NULL
+ * arrays, then the arrays (rows, rows*H, rows*H_kv, rows, B, B, B, B*max_pages). */
+int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32_t* max_pages,
+                           uint32_t* ids, uint32_t* posq, uint32_t* posk, uint32_t* slots,
+                           uint32_t* lengths, uint32_t* extents, uint32_t* last,
+                           uint32_t* pages);
+
+/* ---- measurement ------------------------------------------------------- */
+/* Brackets every attention launch of tgohip_step with HIP events on the
+ * context's stream and accumulates its duration and its algorithmic bytes
+ * (every cached position a claimed row reads, K and V of all kv heads, once;
+ * plus q read and the output written). Turning it on resets the sums. */
+int tgohip_set_profile(tgohip_ctx* ctx, int on);
+int tgohip_profile_read(tgohip_ctx* ctx, double* attn_ms, double* attn_bytes,
+                        int64_t* launches);
+/* Fills positions [0, positions) of every layer's K and V with seeded f16
+ * N(0,1)*sigma: the context of sequences admitted already prefilled. */
+int tgohip_kv_synth(tgohip_ctx* ctx, uint64_t seed, double sigma, int positions);
+
 /* ---- weight conversion at load: weights/convert.go ---------------------- */
 /* f32ToF16Bits over an array (weights/convert.go:133-180): RNE, saturate to
  * +-65504 (counted), flush below 2^-14 keeping sign, NaN -> 0x7e00. */

@@ -107,6 +107,13 @@ def lib():
         "tgohip_sched_feed": (I, [P, I, I]),
         "tgohip_sched_length": (I, [P, I]),
         "tgohip_sched_step": (I, [P, P, P, P, P, P, ctypes.POINTER(Timings)]),
+        "tgohip_sched_admit_prefilled": (I, [P, P, I, I, I]),
+        "tgohip_sched_prefilling": (I, [P]),
+        "tgohip_sched_live": (I, [P]),
+        "tgohip_sched_last_step": (I, [P, P, P, P, P, P, P, P, P, P, P, P]),
+        "tgohip_set_profile": (I, [P, I]),
+        "tgohip_profile_read": (I, [P, P, P, P]),
+        "tgohip_kv_synth": (I, [P, U64, D, I]),
         "tgohip_to_f16": (ctypes.c_size_t, [P, P, ctypes.c_size_t]),
         "tgohip_quantize_int8": (None, [P, ctypes.c_size_t, P, P]),
         "tgohip_quantize_int4": (None, [P, ctypes.c_size_t, P, P, P]),
@@ -365,6 +372,18 @@ class Context:
     def kv_alloc(self, positions):
         check(lib().tgohip_kv_alloc(self.h, positions))
 
+    def kv_synth(self, seed, sigma, positions):
+        check(lib().tgohip_kv_synth(self.h, seed, sigma, positions))
+
+    def set_profile(self, on):
+        check(lib().tgohip_set_profile(self.h, 1 if on else 0))
+
+    def profile_read(self):
+        ms, by, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        check(lib().tgohip_profile_read(self.h, ctypes.byref(ms), ctypes.byref(by),
+                                        ctypes.byref(n)))
+        return ms.value, by.value, n.value
+
     def kv_pointers(self):
         k, v, n = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int()
         check(lib().tgohip_kv_pointers(self.h, ctypes.byref(k), ctypes.byref(v), ctypes.byref(n)))
@@ -437,6 +456,36 @@ class Scheduler:
     def admit(self, prompt, reserve=0):
         a = i32(prompt or [0])
         return check(lib().tgohip_sched_admit(self.h, ptr(a), len(prompt), reserve))
+
+    def admit_prefilled(self, prompt, feed, reserve=0):
+        a = i32(prompt or [0])
+        return check(lib().tgohip_sched_admit_prefilled(self.h, ptr(a), len(prompt), reserve,
+                                                        feed))
+
+    def prefilling(self):
+        return lib().tgohip_sched_prefilling(self.h)
+
+    def live(self):
+        return lib().tgohip_sched_live(self.h)
+
+    def last_step(self):
+        """The ports of the last step: (dict of arrays, pages, max_pages)."""
+        r, b, mp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        L = lib()
+        L.tgohip_sched_last_step(self.h, ctypes.byref(r), ctypes.byref(b), ctypes.byref(mp),
+                                 *([None] * 8))
+        cfg = self.ctx.cfg
+        rows, B, maxp = r.value, b.value, mp.value
+        st = dict(ids=np.zeros(rows, np.uint32), posq=np.zeros(rows * cfg["heads"], np.uint32),
+                  posk=np.zeros(rows * cfg["kv_heads"], np.uint32),
+                  slots=np.zeros(rows, np.uint32), lengths=np.zeros(B, np.uint32),
+                  extents=np.zeros(B, np.uint32), last=np.zeros(B, np.uint32))
+        pages = np.zeros(B * maxp, np.uint32)
+        L.tgohip_sched_last_step(self.h, ctypes.byref(r), ctypes.byref(b), ctypes.byref(mp),
+                                 ptr(st["ids"]), ptr(st["posq"]), ptr(st["posk"]),
+                                 ptr(st["slots"]), ptr(st["lengths"]), ptr(st["extents"]),
+                                 ptr(st["last"]), ptr(pages))
+        return st, pages, maxp
 
     def finish(self, slot):
         check(lib().tgohip_sched_finish(self.h, slot))

@@ -55,7 +55,7 @@ struct AttnCombine {
 
 constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
 constexpr int kAttnSplit = 512;   // positions per split of a decode-style item
-constexpr int kAttnRowsP = 128;   // rows per prefill-style item (4 waves x 32)
+constexpr int kAttnRowsP = 64;    // rows per prefill-style item (4 waves x 16)
 constexpr int kHeadDim = 128;
 
 struct AttnPlan {

@@ -71,7 +71,7 @@ __device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const
   }
 }
 
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[32768 + 512];
   half_t* Ks = (half_t*)smem;
   half_t* Vs = (half_t*)(smem + 16384);
@@ -83,19 +83,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const int L = (int)a.lengths[s], n = (int)a.extents[s], cu = a.cu[s];
   const int R = it.ntok * G;
   const bool pmode = it.mode == 1;
-  const int rowbase = pmode ? wave * 32 : 0;
+  // Each wave owns one block of 16 rows: in a prefill-style item the four
+  // waves own rows [16w, 16w+16); in a decode-style item all four hold the
+  // same rows and take different positions.
+  const int r = (pmode ? wave * 16 : 0) + li;
+  const bool valid = r < R;
+  const int tok = it.tok0 + (valid ? r / G : 0);
+  const int head = kvh * G + (valid ? r % G : 0);
+  const int lim = valid ? (L - n + tok) : -1;
 
-  // Q as the B operand of S^T = K.Q^T: lane holds row li of its n-block, dims
-  // 32c + 8lg + [0,8). Scaled by scale*log2(e) and split hi + lo.
-  half8_t qh[2][4], ql[2][4];
-  int lim[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; nb++) {
-    const int r = rowbase + nb * 16 + li;
-    const bool valid = (pmode || nb == 0) && r < R;
-    const int tok = it.tok0 + (valid ? r / G : 0);
-    const int head = kvh * G + (valid ? r % G : 0);
-    lim[nb] = valid ? (L - n + tok) : -1;
+  // Q as the B operand of S^T = K.Q^T: lane holds row li, dims 32c + 8lg +
+  // [0,8), scaled by scale*log2(e) and split hi + lo.
+  half8_t qh[4], ql[4];
+  {
     const size_t qoff = ((size_t)(cu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -120,18 +120,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       for (int j = 0; j < 8; j++) {
         const float xs = x[j] * a.qscale;
         const half_t hi = (half_t)xs;
-        qh[nb][c][j] = hi;
-        ql[nb][c][j] = (half_t)(xs - (float)hi);
+        qh[c][j] = hi;
+        ql[c][j] = (half_t)(xs - (float)hi);
       }
     }
   }
 
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  float4_t o[2][8];
+  float m = -INFINITY, l = 0.f;
+  float4_t o[8];
 #pragma unroll
-  for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-    for (int db = 0; db < 8; db++) o[nb][db] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < 8; db++) o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t* prow = a.pages + (size_t)s * a.max_pages;
   uint4 kreg[4], vreg[4];
@@ -168,68 +166,57 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int mb0 = pmode ? 0 : wave, mb1 = pmode ? 4 : wave + 1;
     for (int mb = mb0; mb < mb1; mb++) {
       if (t0 + mb * 16 >= it.kv_hi) break;
-      half8_t ka[4];
+      float4_t st = {0.f, 0.f, 0.f, 0.f};
       {
         const int pos = mb * 16 + li;
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          ka[c] = *(const half8_t*)(Ks + (pos * 16 + ((4 * c + lg) ^ (pos & 15))) * 8);
+        for (int c = 0; c < 4; c++) {
+          const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((4 * c + lg) ^ (pos & 15))) * 8);
+          st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[c], st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], st, 0, 0, 0);
+        }
       }
-      // V^T fragments for this block of 16 positions: lane holds
-      // V[pos 4lg+e][dim 16db+li] for e = 0..3.
-      half4_t va[8];
+      float sv[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int pabs = t0 + mb * 16 + 4 * lg + q;
+        const bool ok = pabs <= lim && pabs < it.kv_hi;
+        sv[q] = ok ? st[q] : -INFINITY;
+        tmax = fmaxf(tmax, sv[q]);
+      }
+      tmax = wave_max16x(tmax);
+      const float mnew = fmaxf(m, tmax);
+      float alpha = 1.f;
+      half4_t pb;
+      float psum = 0.f;
+      if (mnew == -INFINITY) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) pb[q] = (half_t)0.f;
+      } else {
+        alpha = exp2f(m - mnew);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float p = exp2f(sv[q] - mnew);
+          psum += p;
+          pb[q] = (half_t)p;
+        }
+      }
+      psum = wave_sum16x(psum);
+      l = l * alpha + psum;
+      m = mnew;
+      // O^T += V^T . P^T: the A operand holds V[pos 4lg+e][dim 16db+li].
 #pragma unroll
       for (int db = 0; db < 8; db++) {
         const int d = db * 16 + li;
+        half4_t va;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int pos = mb * 16 + 4 * lg + e;
-          va[db][e] = Vs[(pos * 16 + ((d >> 3) ^ (pos & 15))) * 8 + (d & 7)];
+          va[e] = Vs[(pos * 16 + ((d >> 3) ^ (pos & 15))) * 8 + (d & 7)];
         }
-      }
-#pragma unroll
-      for (int nb = 0; nb < 2; nb++) {
-        if (nb == 1 && !pmode) break;
-        float4_t st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], qh[nb][c], st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], ql[nb][c], st, 0, 0, 0);
-        }
-        float sv[4];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int pabs = t0 + mb * 16 + 4 * lg + r;
-          const bool ok = pabs <= lim[nb] && pabs < it.kv_hi;
-          sv[r] = ok ? st[r] : -INFINITY;
-          tmax = fmaxf(tmax, sv[r]);
-        }
-        tmax = wave_max16x(tmax);
-        const float mnew = fmaxf(m[nb], tmax);
-        float alpha = 1.f;
-        half4_t pb;
-        float psum = 0.f;
-        if (mnew == -INFINITY) {
-#pragma unroll
-          for (int r = 0; r < 4; r++) pb[r] = (half_t)0.f;
-        } else {
-          alpha = exp2f(m[nb] - mnew);
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float p = exp2f(sv[r] - mnew);
-            psum += p;
-            pb[r] = (half_t)p;
-          }
-        }
-        psum = wave_sum16x(psum);
-        l[nb] = l[nb] * alpha + psum;
-        m[nb] = mnew;
-#pragma unroll
-        for (int db = 0; db < 8; db++) {
-          o[nb][db] *= alpha;
-          o[nb][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[db], pb, o[nb][db], 0, 0, 0);
-        }
+        o[db] *= alpha;
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[db], 0, 0, 0);
       }
     }
   }
@@ -242,10 +229,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int db = 0; db < 8; db++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) Os[(wave * 16 + li) * 128 + db * 16 + 4 * lg + r] = o[0][db][r];
+      for (int q = 0; q < 4; q++) Os[(wave * 16 + li) * 128 + db * 16 + 4 * lg + q] = o[db][q];
     if (lg == 0) {
-      Ms[wave * 16 + li] = m[0];
-      Ms[64 + wave * 16 + li] = l[0];
+      Ms[wave * 16 + li] = m;
+      Ms[64 + wave * 16 + li] = l;
     }
     __syncthreads();
     const int row = tid >> 4, d0 = (tid & 15) * 8;
@@ -267,8 +254,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) acc[j] *= inv;
-        const int tok = it.tok0 + row / G, head = kvh * G + row % G;
-        store_out8(a.out, a.out_f16, ((size_t)(cu + tok) * a.H + head) * kHeadDim + d0, acc);
+        const int tk = it.tok0 + row / G, hd = kvh * G + row % G;
+        store_out8(a.out, a.out_f16, ((size_t)(cu + tk) * a.H + hd) * kHeadDim + d0, acc);
       } else {
         float* po = a.part_o + ((size_t)it.part * 16 + row) * 128 + d0;
 #pragma unroll
@@ -279,25 +266,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
       }
     }
-  } else {
+  } else if (valid) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const size_t base = ((size_t)(cu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      const int r = rowbase + nb * 16 + li;
-      if (r >= R) continue;
-      const int tok = it.tok0 + r / G, head = kvh * G + r % G;
-      const float inv = l[nb] > 0.f ? 1.f / l[nb] : 0.f;
-      const size_t base = ((size_t)(cu + tok) * a.H + head) * kHeadDim;
+    for (int db = 0; db < 8; db++) {
+      const size_t off = base + db * 16 + 4 * lg;
+      if (a.out_f16) {
+        half4_t hv;
 #pragma unroll
-      for (int db = 0; db < 8; db++) {
-        const size_t off = base + db * 16 + 4 * lg;
-        if (a.out_f16) {
-          half4_t h;
-#pragma unroll
-          for (int r2 = 0; r2 < 4; r2++) h[r2] = (half_t)(o[nb][db][r2] * inv);
-          *(half4_t*)((half_t*)a.out + off) = h;
-        } else {
-          *(float4_t*)((float*)a.out + off) = o[nb][db] * inv;
-        }
+        for (int q = 0; q < 4; q++) hv[q] = (half_t)(o[db][q] * inv);
+        *(half4_t*)((half_t*)a.out + off) = hv;
+      } else {
+        *(float4_t*)((float*)a.out + off) = o[db] * inv;
       }
     }
   }

@@ -93,6 +93,11 @@ struct tgohip_ctx {
   std::vector<void*> allocs;  // weight and gain allocations owned by the context
   std::map<int, PackedWeight> handles;
   int next_handle = 1;
+  // profiling: HIP events around every attention launch of a step
+  bool profile = false;
+  std::vector<hipEvent_t> prof_ev;
+  double prof_attn_ms = 0, prof_attn_bytes = 0;
+  int64_t prof_attn_launches = 0;
 };
 
 namespace {
@@ -449,6 +454,7 @@ void tgohip_close(tgohip_ctx* c) {
   if (c->kc) (void)hipFree(c->kc);
   if (c->vc) (void)hipFree(c->vc);
   if (c->pinned) (void)hipHostFree(c->pinned);
+  for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   (void)hipEventDestroy(c->staged);
   (void)hipEventDestroy(c->ev0);
   (void)hipEventDestroy(c->ev1);
@@ -739,6 +745,19 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   float* ws = (float*)c->gemm_ws.p;
   const size_t wsb = c->gemm_ws.bytes;
 
+  // Algorithmic bytes of one attention launch: every cached position a
+  // claimed row reads, once (K and V, all kv heads), plus q read and out written.
+  double attn_bytes = 0;
+  if (c->profile) {
+    for (int b = 0; b < B; b++)
+      if (s->extents[b] > 0) attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
+    attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (4 + (f32act ? 4 : 2));
+    while ((int)c->prof_ev.size() < 2 * m.layers) {
+      hipEvent_t e;
+      TGOHIP_HIP(hipEventCreate(&e));
+      c->prof_ev.push_back(e);
+    }
+  }
   launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st);
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
@@ -749,9 +768,11 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
                   (float*)c->q.p, c->kc + l * layer_kv, c->vc + l * layer_kv, m.heads, m.kv_heads,
                   c->kv_positions, m.rms_eps};
     launch_qk_rope_kv(qa, T, st);
+    if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l], st));
     if ((rc = attn_enqueue(plan, dp, c->q.p, 0, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
+    if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l + 1], st));
     if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st))) return rc;
     launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st);
     if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, T, c->act.p,
@@ -773,6 +794,15 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
     TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)B * m.vocab * 4, hipMemcpyDeviceToHost));
   if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)B * 4, hipMemcpyDeviceToHost));
   const auto t_end = clk::now();
+  if (c->profile) {
+    for (int l = 0; l < m.layers; l++) {
+      float ms = 0;
+      TGOHIP_HIP(hipEventElapsedTime(&ms, c->prof_ev[2 * l], c->prof_ev[2 * l + 1]));
+      c->prof_attn_ms += ms;
+    }
+    c->prof_attn_launches += m.layers;
+    c->prof_attn_bytes += attn_bytes * m.layers;
+  }
   if (tm) {
     float dev_ms = 0;
     (void)hipEventElapsedTime(&dev_ms, c->ev0, c->ev1);
@@ -1151,6 +1181,97 @@ int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, in
     produced++;
   }
   return produced;
+}
+
+}  // extern "C"
+
+// ===========================================================================
+// measurement and benchmark helpers
+// ===========================================================================
+extern "C" {
+
+int tgohip_set_profile(tgohip_ctx* c, int on) {
+  c->profile = on != 0;
+  c->prof_attn_ms = 0;
+  c->prof_attn_bytes = 0;
+  c->prof_attn_launches = 0;
+  return 0;
+}
+
+int tgohip_profile_read(tgohip_ctx* c, double* attn_ms, double* attn_bytes, int64_t* launches) {
+  *attn_ms = c->prof_attn_ms;
+  *attn_bytes = c->prof_attn_bytes;
+  *launches = c->prof_attn_launches;
+  return 0;
+}
+
+// Fills positions [0, positions) of every layer of the K and V pools with
+// loader-rule f16 of N(0,1)*sigma from (seed, stream 0x4b / 0x56): the synthetic
+// context of sequences admitted already prefilled.
+int tgohip_kv_synth(tgohip_ctx* c, uint64_t seed, double sigma, int positions) {
+  if (!c->kc) return fail(TGOHIP_ESTATE, "kv_synth: allocate the pool first");
+  positions = std::min(positions, c->kv_positions);
+  const size_t row = (size_t)c->cfg.kv_heads * kHeadDim;
+  for (int l = 0; l < c->cfg.layers; l++) {
+    const size_t off = (size_t)l * c->kv_positions * row;
+    // one stream per layer so a layer's contents do not depend on the pool size
+    launch_synth_f16(seed, 0x4b00 + (uint64_t)l, (size_t)positions * row, sigma,
+                     (uint16_t*)(c->kc + off), c->stream);
+    launch_synth_f16(seed, 0x5600 + (uint64_t)l, (size_t)positions * row, sigma,
+                     (uint16_t*)(c->vc + off), c->stream);
+  }
+  TGOHIP_HIP(hipGetLastError());
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+// Admits a sequence whose prompt's KV is already in the pool (restored or
+// synthetic): the lease covers the prompt and the slot starts decoding, its
+// first fed token being `feed`.
+int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, int reserve,
+                                 int feed) {
+  const int slot = tgohip_sched_admit(s, prompt, n, reserve);
+  if (slot < 0) return slot;
+  SchedSlot& sl = s->slots[slot];
+  sl.prefilled = n;
+  sl.length = n;
+  sl.feed = feed;
+  return slot;
+}
+
+int tgohip_sched_prefilling(tgohip_sched* s) {
+  int k = 0;
+  for (auto& sl : s->slots)
+    if (sl.live && sl.prefilled < (int)sl.prompt.size()) k++;
+  return k;
+}
+
+int tgohip_sched_live(tgohip_sched* s) {
+  int k = 0;
+  for (auto& sl : s->slots) k += sl.live ? 1 : 0;
+  return k;
+}
+
+// The ports of the scheduler's last step (for replaying it elsewhere, e.g. on
+// the CPU restatement). Pass NULL arrays to learn the sizes first.
+int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32_t* max_pages,
+                           uint32_t* ids, uint32_t* posq, uint32_t* posk, uint32_t* slots,
+                           uint32_t* lengths, uint32_t* extents, uint32_t* last, uint32_t* pages) {
+  *rows = (int32_t)s->ids.size();
+  *batch = (int32_t)s->lengths.size();
+  *max_pages = s->ctx->kv_positions / s->ctx->cfg.block;
+  auto cp = [](uint32_t* dst, const std::vector<uint32_t>& v) {
+    if (dst) std::memcpy(dst, v.data(), v.size() * 4);
+  };
+  cp(ids, s->ids);
+  cp(posq, s->posq);
+  cp(posk, s->posk);
+  cp(slots, s->slotv);
+  cp(lengths, s->lengths);
+  cp(extents, s->extents);
+  cp(last, s->last);
+  cp(pages, s->table);
+  return 0;
 }
 
 }  // extern "C"
