@@ -54,7 +54,7 @@ struct AttnCombine {
 };
 
 constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
-constexpr int kAttnSplit = 512;   // positions per split of a decode-style item
+constexpr int kAttnSplit = 1024;  // positions per part of a context-split item
 constexpr int kAttnRowsP = 64;    // rows per prefill-style item (4 waves x 16)
 constexpr int kHeadDim = 128;
 

@@ -95,74 +95,87 @@ __device__ __forceinline__ half8_t deq_i8(uint32_t w0, uint32_t w1, half8_t s) {
   return o;
 }
 
-// Per-form payload sizes (bytes per lane per (nb, ks)).
-template <int FORM> struct Payload;
-template <> struct Payload<TGOHIP_FORM_F16> { static constexpr int bytes = 64; };
-template <> struct Payload<TGOHIP_FORM_I8> { static constexpr int bytes = 32; };
-template <> struct Payload<TGOHIP_FORM_I4_TGO> { static constexpr int bytes = 16; };
-template <> struct Payload<TGOHIP_FORM_I4_SYM> { static constexpr int bytes = 16; };
+// The lane's raw material for one (nb, ks): payload plus the scales it needs,
+// sized per form so no register is spent on another form's fields.
+template <int FORM> struct BRaw;
+template <> struct BRaw<TGOHIP_FORM_F16> { uint4 p[4]; };
+template <> struct BRaw<TGOHIP_FORM_I8> { uint4 p[2]; uint4 s[4]; };
+template <> struct BRaw<TGOHIP_FORM_I4_TGO> { uint4 p; uint4 s[4]; uint4 z[4]; };
+template <> struct BRaw<TGOHIP_FORM_I4_SYM> { uint4 p; uint32_t s; };
 
-// The lane's raw material for one (nb, ks): payload plus scales.
-template <int FORM>
-struct BRaw {
-  uint4 p[Payload<FORM>::bytes / 16];
-  uint4 s[4];   // per-k scales (I8, I4_TGO): 8 halves per substep; I4_SYM uses s[0].x
-  uint4 z[4];   // per-k zero+1024 (I4_TGO)
-};
-
-template <int FORM>
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
-                                          BRaw<FORM>& r) {
+                                          BRaw<TGOHIP_FORM_F16>& r) {
+  const size_t slot = ((size_t)nb * (g.K / 64) + ks) * 64 + lane;
+  const uint4* pp = (const uint4*)((const char*)g.wp + slot * 64);
+#pragma unroll
+  for (int i = 0; i < 4; i++) r.p[i] = pp[i];
+}
+__device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
+                                          BRaw<TGOHIP_FORM_I8>& r) {
   const int KS = g.K / 64;
   const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
-  const uint4* pp = (const uint4*)((const char*)g.wp + slot * Payload<FORM>::bytes);
+  const uint4* pp = (const uint4*)((const char*)g.wp + slot * 32);
+  r.p[0] = pp[0];
+  r.p[1] = pp[1];
+  const int h = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < Payload<FORM>::bytes / 16; i++) r.p[i] = pp[i];
-  if (FORM == TGOHIP_FORM_I4_SYM) {
-    const uint32_t* sp = (const uint32_t*)(g.ws) + ((size_t)nb * KS + ks) * 32 + (lane & 31);
-    r.s[0].x = *sp;
-  } else if (FORM == TGOHIP_FORM_I8 || FORM == TGOHIP_FORM_I4_TGO) {
-    const int h = lane >> 5;
+  for (int j = 0; j < 4; j++) r.s[j] = *(const uint4*)(g.ws + ((((size_t)nb * KS + ks) * 4 + j) * 2 + h) * 8);
+}
+__device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
+                                          BRaw<TGOHIP_FORM_I4_TGO>& r) {
+  const int KS = g.K / 64;
+  const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
+  r.p = *(const uint4*)((const char*)g.wp + slot * 16);
+  const int h = lane >> 5;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const size_t o = ((((size_t)nb * KS + ks) * 4 + j) * 2 + h) * 8;
-      r.s[j] = *(const uint4*)(g.ws + o);
-      if (FORM == TGOHIP_FORM_I4_TGO) r.z[j] = *(const uint4*)(g.wz + o);
-    }
+  for (int j = 0; j < 4; j++) {
+    const size_t o = ((((size_t)nb * KS + ks) * 4 + j) * 2 + h) * 8;
+    r.s[j] = *(const uint4*)(g.ws + o);
+    r.z[j] = *(const uint4*)(g.wz + o);
   }
 }
+__device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
+                                          BRaw<TGOHIP_FORM_I4_SYM>& r) {
+  const int KS = g.K / 64;
+  const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
+  r.p = *(const uint4*)((const char*)g.wp + slot * 16);
+  r.s = *((const uint32_t*)(g.ws) + ((size_t)nb * KS + ks) * 32 + (lane & 31));
+}
 
-template <int FORM>
-__device__ __forceinline__ half8_t bfrag(const BRaw<FORM>& r, int j) {
-  union U { uint4 u; half8_t h; };
-  if (FORM == TGOHIP_FORM_F16) {
-    U c;
-    c.u = r.p[j];
-    return c.h;
-  } else if (FORM == TGOHIP_FORM_I4_SYM) {
-    const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
-    union { uint32_t u; half2_t h; } sc;
-    sc.u = r.s[0].x;
-    return deq_i4_sym(w, j < 2 ? sc.h[0] : sc.h[1]);
-  } else if (FORM == TGOHIP_FORM_I4_TGO) {
-    const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
-    U s, z;
-    s.u = r.s[j];
-    z.u = r.z[j];
-    return deq_i4_asym(w, s.h, z.h);
-  } else {
-    const uint4 q = r.p[j >> 1];
-    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
-    U s;
-    s.u = r.s[j];
-    return deq_i8(w0, w1, s.h);
-  }
+__device__ __forceinline__ uint32_t word_of(const uint4& p, int j) {
+  return j == 0 ? p.x : j == 1 ? p.y : j == 2 ? p.z : p.w;
+}
+
+union U16B { uint4 u; half8_t h; };
+
+__device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_F16>& r, int j) {
+  U16B c;
+  c.u = r.p[j];
+  return c.h;
+}
+__device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I4_SYM>& r, int j) {
+  union { uint32_t u; half2_t h; } sc;
+  sc.u = r.s;
+  return deq_i4_sym(word_of(r.p, j), j < 2 ? sc.h[0] : sc.h[1]);
+}
+__device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I4_TGO>& r, int j) {
+  U16B s, z;
+  s.u = r.s[j];
+  z.u = r.z[j];
+  return deq_i4_asym(word_of(r.p, j), s.h, z.h);
+}
+__device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I8>& r, int j) {
+  const uint4 q = r.p[j >> 1];
+  const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
+  U16B s;
+  s.u = r.s[j];
+  return deq_i8(w0, w1, s.h);
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
 
 template <int FORM, int MW, bool ASPLIT, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   constexpr int MB = MW / 32;
   constexpr int APLANES = ASPLIT ? 2 : 1;
   __shared__ __attribute__((aligned(16))) half_t As[2][APLANES][MW * 64];
@@ -233,7 +246,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     load_a(ks0);
 #pragma unroll
     for (int b = 0; b < 2; b++)
-      if (nbv[b]) load_braw<FORM>(g, nbw0 + b, ks0, lane, bcur[b]);
+      if (nbv[b]) load_braw(g, nbw0 + b, ks0, lane, bcur[b]);
     store_a(0);
   }
   __syncthreads();
@@ -244,13 +257,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       load_a(ks + 1);
 #pragma unroll
       for (int b = 0; b < 2; b++)
-        if (nbv[b]) load_braw<FORM>(g, nbw0 + b, ks + 1, lane, bnext[b]);
+        if (nbv[b]) load_braw(g, nbw0 + b, ks + 1, lane, bnext[b]);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       half8_t bf[2];
 #pragma unroll
-      for (int b = 0; b < 2; b++) bf[b] = bfrag<FORM>(bcur[b], j);
+      for (int b = 0; b < 2; b++) bf[b] = bfrag(bcur[b], j);
 #pragma unroll
       for (int mb = 0; mb < MB; mb++) {
         const int row = mb * 32 + c32;
@@ -429,39 +442,37 @@ __global__ void dequant_kernel(GemmArgs g, void* out) {
   const int lane = (int)(t % 64), ks = (int)((t / 64) % KS), nb = (int)(t / 64 / KS);
   const int h = lane >> 5, n = nb * 32 + (lane & 31);
   BRaw<FORM> r;
-  load_braw<FORM>(g, nb, ks, lane, r);
+  load_braw(g, nb, ks, lane, r);
   for (int j = 0; j < 4; j++) {
     const int kb = ks * 64 + 16 * j + 8 * h;
     if (F16OUT) {
-      const half8_t f = bfrag<FORM>(r, j);
+      const half8_t f = bfrag(r, j);
       for (int e = 0; e < 8; e++) ((half_t*)out)[(size_t)(kb + e) * g.N + n] = f[e];
     } else {
       for (int e = 0; e < 8; e++) {
         float v;
-        if (FORM == TGOHIP_FORM_F16) {
-          union { uint4 u; half8_t hh; } c;
+        if constexpr (FORM == TGOHIP_FORM_F16) {
+          U16B c;
           c.u = r.p[j];
-          v = (float)c.hh[e];
-        } else if (FORM == TGOHIP_FORM_I4_SYM || FORM == TGOHIP_FORM_I4_TGO) {
-          const uint32_t w = j == 0 ? r.p[0].x : j == 1 ? r.p[0].y : j == 2 ? r.p[0].z : r.p[0].w;
-          const uint32_t q = (w >> (4 * nib_slot(e))) & 15u;
-          if (FORM == TGOHIP_FORM_I4_SYM) {
-            union { uint32_t u; half2_t hh; } sc;
-            sc.u = r.s[0].x;
-            v = (float)((int)q - 8) * (float)(j < 2 ? sc.hh[0] : sc.hh[1]);
-          } else {
-            union { uint4 u; half8_t hh; } s, z;
-            s.u = r.s[j];
-            z.u = r.z[j];
-            v = ((float)q - ((float)z.hh[e] - 1024.f)) * (float)s.hh[e];
-          }
+          v = (float)c.h[e];
+        } else if constexpr (FORM == TGOHIP_FORM_I4_SYM) {
+          const uint32_t q = (word_of(r.p, j) >> (4 * nib_slot(e))) & 15u;
+          union { uint32_t u; half2_t hh; } sc;
+          sc.u = r.s;
+          v = (float)((int)q - 8) * (float)(j < 2 ? sc.hh[0] : sc.hh[1]);
+        } else if constexpr (FORM == TGOHIP_FORM_I4_TGO) {
+          const uint32_t q = (word_of(r.p, j) >> (4 * nib_slot(e))) & 15u;
+          U16B sv, zv;
+          sv.u = r.s[j];
+          zv.u = r.z[j];
+          v = ((float)q - ((float)zv.h[e] - 1024.f)) * (float)sv.h[e];
         } else {
           const uint4 qq = r.p[j >> 1];
           const uint32_t w = (e < 4) ? ((j & 1) ? qq.z : qq.x) : ((j & 1) ? qq.w : qq.y);
-          const uint32_t b = (w >> (8 * byte_slot(e & 3))) & 255u;
-          union { uint4 u; half8_t hh; } s;
-          s.u = r.s[j];
-          v = (float)((int)b - 128) * (float)s.hh[e];
+          const uint32_t bb = (w >> (8 * byte_slot(e & 3))) & 255u;
+          U16B sv;
+          sv.u = r.s[j];
+          v = (float)((int)bb - 128) * (float)sv.h[e];
         }
         ((float*)out)[(size_t)(kb + e) * g.N + n] = v;
       }

@@ -389,9 +389,9 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
 }
 
 int ensure_attn_parts(tgohip_ctx* c, int parts) {
-  int rc = c->part_o.ensure((size_t)std::max(parts, 1) * 16 * 128 * 4);
+  int rc = c->part_o.ensure((size_t)std::max(parts, 1) * 64 * 128 * 4);
   if (rc) return rc;
-  return c->part_ml.ensure((size_t)std::max(parts, 1) * 32 * 4);
+  return c->part_ml.ensure((size_t)std::max(parts, 1) * 128 * 4);
 }
 
 }  // namespace
@@ -650,6 +650,9 @@ int tgohip_synth_weights(tgohip_ctx* c, uint64_t seed, int form, double sigma) {
 
 int tgohip_kv_alloc(tgohip_ctx* c, int positions) {
   if (!c->configured) return fail(TGOHIP_ESTATE, "kv_alloc: configure the context first");
+  if ((int64_t)positions * c->cfg.kv_heads * kHeadDim >= (int64_t)1 << 31)
+    return fail(TGOHIP_EINVAL, "kv_alloc: one layer of the pool is addressed with 32-bit element "
+                               "offsets; " + std::to_string(positions) + " positions exceed it");
   const int blocks = positions / c->cfg.block;
   if (blocks < 1)
     return fail(TGOHIP_EINVAL, "kv_alloc: a shared cache of " + std::to_string(positions) +
@@ -822,6 +825,8 @@ int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int
     return fail(TGOHIP_EINVAL, "attention: head_dim is " + std::to_string(head_dim) +
                                    "; the kernel is built for 128");
   if (T < 0 || B < 0 || capacity <= 0) return fail(TGOHIP_EINVAL, "attention: T, B and capacity");
+  if ((int64_t)capacity * H_kv * kHeadDim >= (int64_t)1 << 31)
+    return fail(TGOHIP_EINVAL, "attention: the cache view exceeds 32-bit element offsets");
   AttnPlan plan;
   int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan);
   if (rc) return rc;
