@@ -39,6 +39,8 @@ def _load():
         "orc_f16_to_f32": (F, [ctypes.c_uint16]),
         "orc_to_f16": (ctypes.c_size_t, [P, P, ctypes.c_size_t]),
         "orc_transpose": (None, [P, P, I, I]),
+        "orc_f16_ieee_bits_array": (None, [P, P, ctypes.c_size_t]),
+        "orc_f16_loader_bits_array": (None, [P, P, ctypes.c_size_t]),
         "orc_permute_heads": (I, [P, ctypes.c_size_t, I, I]),
         "orc_quantize_int8": (None, [P, ctypes.c_size_t, P, P]),
         "orc_dequant_int8": (None, [P, P, ctypes.c_size_t, P]),

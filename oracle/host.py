@@ -192,7 +192,11 @@ def chain_all(seed, ids, block):
 
 
 class Exhausted(Exception):
-    pass
+    """prefix.ErrExhausted (internal/prefix/prefix.go:54)."""
+
+
+class Released(Exception):
+    """prefix.ErrReleased (internal/prefix/lease.go): the lease was released."""
 
 
 class Pool:
@@ -311,6 +315,8 @@ class Lease:
 
     def grow(self, n):
         p = self.pool
+        if self.released:
+            raise Released()
         if n == 0:
             return
         want = (len(self.ids) + n + p.block - 1) // p.block
@@ -322,6 +328,8 @@ class Lease:
 
     def commit(self, ids):
         p = self.pool
+        if self.released:
+            raise Released()
         if not ids:
             return
         want = (len(self.ids) + len(ids) + p.block - 1) // p.block

@@ -12,7 +12,8 @@
  *   orc_f32_to_f16_bits   pinned: known bits of weights/convert_test.go:106-250,
  *                         exhaustive agreement with IEEE RNE on the normal range
  *                         (numpy float16) and the carve-outs (saturate, FTZ).
- *   orc_f32_to_f16_ieee   pinned: exhaustive over all 2^32 f32 against numpy.
+ *   orc_f32_to_f16_ieee   pinned: against numpy over every f32 sign/exponent/top-10-mantissa
+ *                         pattern with 16 low-bit variants (every rounding boundary).
  *   orc_transpose/permute pinned: convert_test.go:261-297 known answers.
  *   orc_quantize_int8     partially pinned: scale = f16(peak/127), reconstruction
  *                         within s/2 (weights/weights_test.go:280-288). The tie
@@ -909,4 +910,14 @@ int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uin
   free(lastrows);
   free(h); free(n); free(q); free(k); free(v); free(a); free(y); free(gt); free(up);
   return 0;
+}
+
+/* Array forms over raw f32 bit patterns (for exhaustive checks). */
+void orc_f16_ieee_bits_array(const uint32_t* bits, uint16_t* out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)n; i++) out[i] = orc_f32_to_f16_ieee(bitsf32(bits[i]));
+}
+void orc_f16_loader_bits_array(const uint32_t* bits, uint16_t* out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)n; i++) out[i] = orc_f32_to_f16_bits(bitsf32(bits[i]), NULL);
 }

@@ -40,6 +40,8 @@ size_t   orc_to_f16(const float* src, uint16_t* dst, size_t n);
 /* IEEE binary16 round-to-nearest-even with overflow to infinity and gradual
  * underflow: the device Cast (accel.ToFloat16) that narrows K/V rows. */
 uint16_t orc_f32_to_f16_ieee(float x);
+void     orc_f16_ieee_bits_array(const uint32_t* bits, uint16_t* out, size_t n);
+void     orc_f16_loader_bits_array(const uint32_t* bits, uint16_t* out, size_t n);
 void     orc_transpose(const float* src, float* dst, int rows, int cols);
 int      orc_permute_heads(float* x, size_t n, int last_axis, int head_dim);
 

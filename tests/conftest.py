@@ -29,3 +29,12 @@ def ctx(torch_gpu):
     c.set_stream(torch_gpu.cuda.current_stream().cuda_stream)
     yield c
     c.close()
+
+
+def pytest_sessionstart(session):
+    """Build the product library and the oracle if nothing is built yet (a fresh checkout);
+    an existing build is used as it is."""
+    import tgo_amd
+    if not os.path.exists(tgo_amd.LIB_PATH):
+        from tgo_amd import build
+        build.build()
