@@ -61,7 +61,24 @@ def parse():
                    help="0: f16 activations into the MFMA (default); 1: f32 activations (hi+lo)")
     p.add_argument("--form", type=int, default=3, help="weight form (3: int4 sym g32-K, 2: tgo int4)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="before the workload, run one plain f32 copy kernel (torch.neg) over this "
+                        "many MiB: the known-size dispatch that scales the HBM byte counters")
     return p.parse_args()
+
+
+def copy_probe(mib):
+    """One elementwise kernel that reads and writes exactly mib MiB each (y = -x, f32)."""
+    import torch
+    x = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print("copy probe: %d MiB read + %d MiB written by one torch.neg dispatch" % (mib, mib),
+          file=sys.stderr, flush=True)
+    del x, y
+    torch.cuda.empty_cache()
 
 
 class Workload:
@@ -127,6 +144,18 @@ class Workload:
         return out, prefill, decodes, tm
 
 
+def recorded_traffic():
+    """HBM bytes per attention launch measured with rocprofv3 --pmc on this workload
+    (FETCH_SIZE + WRITE_SIZE, each scaled by a copy probe), as profiles/ records it."""
+    path = os.path.join(ROOT, "profiles", "attn_kernel_c4_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch attn_kernel:"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(st, pages, max_pages, out_tokens, form):
     """tgo's CPU path restated (oracle/, OpenMP) on one timed step: the step with 1
     and 2 layers, the per-layer time extrapolated to 36 layers."""
@@ -162,6 +191,8 @@ def main():
               "would shard attention by sequence and the projections by column/row with RCCL, "
               "see DESIGN.md)" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
     import tgo_amd
     t_setup = time.perf_counter()
     ctx = tgo_amd.Context(0)
@@ -237,7 +268,10 @@ def main():
             "peak": HBM_PEAK,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE over the first 3 "
+                              "steps of this workload, scaled by a 1 GiB copy probe "
+                              "(profiles/attn_kernel_c4_pmc.txt)",
             "avg_launch_ms": round(avg_attn_ms, 4),
             "algorithmic_bytes_per_launch": round(attn_bytes / max(launches, 1)),
             "launches": launches,

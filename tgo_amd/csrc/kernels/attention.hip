@@ -19,9 +19,10 @@
 //    so probabilities never leave registers; the online-softmax statistics of a
 //    row live in the same lanes as that row's output accumulators.
 //  * Items with at most 16 rows (decodes: 1 token x G query heads) let the four
-//    waves take different positions and merge in LDS; long contexts are split
-//    into 512-position parts merged by a second kernel. Items with more rows
-//    (prefill chunks) give each wave 32 rows and share every staged tile.
+//    waves take different positions and merge in LDS. Items with more rows
+//    (prefill chunks) take 64 rows, 16 per wave, and share every staged tile.
+//    Contexts longer than kAttnSplit positions are split into parts whose
+//    partial (o, m, l) a second kernel merges in part order (deterministic).
 #include "../common.h"
 
 #include <algorithm>
@@ -404,7 +405,8 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
                                    " are not a multiple of kv heads " + std::to_string(Hkv));
   const int G = H / Hkv;
   if (G > kAttnRowsP)
-    return fail(TGOHIP_EINVAL, "attention: a kv head shared by more than 128 query heads");
+    return fail(TGOHIP_EINVAL, "attention: " + std::to_string(G) + " query heads share a kv head; "
+                               "at most " + std::to_string(kAttnRowsP) + " are supported");
   if (block <= 0) return fail(TGOHIP_EINVAL, "attention: block is " + std::to_string(block));
   plan.items.clear();
   plan.combines.clear();
