@@ -152,3 +152,31 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
             assert bool(((y[:, cols].double() - ref).abs() <= tol).all()), M
     finally:
         ctx.weight_free(h)
+
+
+@pytest.mark.parametrize("M", [96, 131, 300, 1152])
+@pytest.mark.parametrize("KN", [(2048, 416), (512, 4096)])
+def test_large_m_tiles_ragged_edges(ctx, torch_gpu, M, KN):
+    """The f16-activation path at M >= 96 (128-row tiles, XCD-dealt, split-K when
+    the tiles alone do not fill the chip): partial row and column tiles and every
+    column checked against the f64 product of the same f16 operands."""
+    torch = torch_gpu
+    import tgo_amd
+    K, N = KN
+    h = ctx.weight_synth(3, K, N, 17, M, 0.02)
+    try:
+        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        ctx.dequant_f16(h, wf)
+        x = torch.randn(M, K, device="cuda").half()
+        y = torch.full((M, N), float("nan"), device="cuda")
+        ctx.linear(h, x, M, y, x_dtype=tgo_amd.F16)
+        y16 = torch.full((M, N), float("nan"), device="cuda", dtype=torch.float16)
+        ctx.linear(h, x, M, y16, x_dtype=tgo_amd.F16, y_dtype=tgo_amd.F16)
+        torch.cuda.synchronize()
+        ref = x.double() @ wf.double()
+        mag = x.double().abs() @ wf.double().abs()
+        tol = 4 * (K ** 0.5) * 2.0 ** -24 * mag
+        assert bool(((y.double() - ref).abs() <= tol).all())
+        assert torch.equal(y16, y.half())
+    finally:
+        ctx.weight_free(h)

@@ -140,6 +140,35 @@ def test_mixed_step_matches_the_cpu_path(torch_gpu, form, precision):
         cpu.close()
 
 
+@pytest.mark.parametrize("form", [3, 0])
+def test_long_chunk_step_matches_the_cpu_path(torch_gpu, form):
+    """A 150-token chunk beside two decodes: the projections run at M >= 96 (the
+    large-M GEMM path for f16 activations, with its f32, residual and SwiGLU
+    epilogues) and the chunk's attention at 64-row items."""
+    cfg = SMALL
+    ctx, cpu = make_pair(torch_gpu, cfg, form, 23, 0)
+    try:
+        engines = [Engine(b, cfg["vocab"], cfg["heads"], cfg["kv_heads"], cfg["positions"],
+                          cfg["block"], 3) for b in (gpu_backend(ctx), cpu_backend(cpu))]
+        rng = np.random.default_rng(40 + form)
+        p0 = [int(t) for t in rng.integers(0, cfg["vocab"], 9)]
+        p1 = [int(t) for t in rng.integers(0, cfg["vocab"], 4)]
+        for e in engines:
+            e.admit(0, p0, 4)
+            e.admit(1, p1, 4)
+        outs = [e.step([(0, p0), (1, p1)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1], "prefill")
+        p2 = [int(t) for t in rng.integers(0, cfg["vocab"], 150)]
+        for e in engines:
+            e.admit(2, p2, 4)
+        t0, t1 = argmax_first(outs[1][0]), argmax_first(outs[1][1])
+        outs = [e.step([(0, [t0]), (1, [t1]), (2, p2)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1, 2], "chunk of 150")
+    finally:
+        ctx.close()
+        cpu.close()
+
+
 def test_batched_step_equals_the_steps_apart(torch_gpu):
     """batch_test.go:72-200: 1e-5 relative and the same argmax, per sequence."""
     cfg = SMALL

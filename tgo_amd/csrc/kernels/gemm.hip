@@ -27,6 +27,7 @@
 #include "../common.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace tgohip {
 
@@ -39,6 +40,7 @@ struct GemmArgs {
   float* part;          // split-K partials [splits][M][N]
   int M, K, N;
   int ksteps_per_split;
+  int map;
 };
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) {
@@ -147,6 +149,7 @@ __device__ __forceinline__ uint32_t word_of(const uint4& p, int j) {
 }
 
 union U16B { uint4 u; half8_t h; };
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_F16>& r, int j) {
   U16B c;
@@ -173,6 +176,60 @@ __device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I8>& r, int j) {
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+
+// 16-byte slot of (row, k-chunk) in an LDS activation tile of 8 chunks per row.
+// The XOR with (row/2) % 8 spreads any 16 consecutive rows of one k-chunk over
+// all 64 banks (a bank row is 256 bytes = two tile rows), so the MFMA operand
+// reads (16 lanes = 16 rows per LDS cycle) and the row-wise stores are
+// conflict-free.
+__device__ __forceinline__ int a_slot(int row, int kc) { return row * 8 + (kc ^ ((row >> 1) & 7)); }
+
+// Epilogue shared by the GEMM kernels. Lane holds D[8*(r/4) + 4*h + (r%4)][c32]
+// of each 32x32 block; a split-K launch writes f32 partials for its split.
+template <int EPI, int MB>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const float16_t (&acc)[MB][2],
+                                              int m0, int nbw0, const bool (&nbv)[2], int h,
+                                              int c32, bool split, int z) {
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (row >= g.M) continue;
+      if (split) {
+        float* dst = g.part + ((size_t)z * g.M + row) * g.N;
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+          if (nbv[b]) dst[(nbw0 + b) * 32 + c32] = acc[mb][b][r];
+      } else if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+        if (nbv[1]) {
+          const float v = silu_f(acc[mb][0][r]) * acc[mb][1][r];
+          const int col = (nbw0 >> 1) * 32 + c32;
+          const size_t o = (size_t)row * (g.N / 2) + col;
+          if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[o] = (half_t)v;
+          else ((float*)g.y)[o] = v;
+        }
+      } else {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          if (!nbv[b]) continue;
+          const size_t o = (size_t)row * g.N + (nbw0 + b) * 32 + c32;
+          if (EPI == EPI_F32) ((float*)g.y)[o] = acc[mb][b][r];
+          else if (EPI == EPI_F16) ((half_t*)g.y)[o] = (half_t)acc[mb][b][r];
+          else ((float*)g.y)[o] += acc[mb][b][r];
+        }
+      }
+    }
+  }
+}
+
+// A workgroup barrier that orders LDS only: global loads in flight stay in
+// flight across it (__syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 template <int FORM, int MW, bool ASPLIT, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
@@ -227,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < ACH; i++) {
       const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
-      const int phys = row * 8 + (kc ^ (row & 7));
+      const int phys = a_slot(row, kc);
 #pragma unroll
       for (int p = 0; p < APLANES; p++) ((uint4*)As[buf][p])[phys] = areg[i][p];
     }
@@ -249,7 +306,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       if (nbv[b]) load_braw(g, nbw0 + b, ks0, lane, bcur[b]);
     store_a(0);
   }
-  __syncthreads();
+  lds_barrier();
   int buf = 0;
   for (int ks = ks0; ks < ks1; ks++) {
     const bool more = ks + 1 < ks1;
@@ -268,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       for (int mb = 0; mb < MB; mb++) {
         const int row = mb * 32 + c32;
         const int kc = 2 * j + h;
-        const int phys = row * 8 + (kc ^ (row & 7));
+        const int phys = a_slot(row, kc);
 #pragma unroll
         for (int p = 0; p < APLANES; p++) {
           const half8_t af = ((const half8_t*)As[buf][p])[phys];
@@ -279,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       }
     }
     if (more) store_a(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
     buf ^= 1;
     if (more) {
 #pragma unroll
@@ -287,39 +344,152 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // Epilogue. Lane holds D[8*(r/4) + 4*h + (r%4)][c32] of each 32x32 block.
-  const bool split = gridDim.z > 1;
+  gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, gridDim.z > 1, blockIdx.z);
+}
+
+// Pipelined variant for f16 activations at larger M (the prefill-sized
+// projections). B fragments (the weight stream) for k-step j are issued at
+// step j-2 into a register ring; A (128 rows x 64 k of f16
+// activations, mostly L2-resident) is issued at step j-1 and written to a
+// double-buffered LDS tile at the end of that step. Barriers order LDS only, so
+// loads stay in flight across them.
+template <int FORM, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
+  constexpr int MW = 128, MB = 4;
+  constexpr int ACH = MW / 32;  // 16-byte A chunks per thread per k-step
+  __shared__ __attribute__((aligned(16))) half_t As[2][MW * 64];
+
+  // XCD x (workgroup b runs on XCD b % 8) owns the column tiles c = x (mod 8):
+  // each weight column tile is streamed into one XCD's L2 and serves every row
+  // tile there. Within an XCD the order is row-major over its columns.
+  int tm, tn;
+  if (g.map == 0) {
+    const int x = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+    const int cols_x = (tiles_n - x + 7) / 8;
+    if (cols_x <= 0 || j >= cols_x * (tiles / tiles_n)) return;
+    tm = j / cols_x;
+    tn = x + 8 * (j - tm * cols_x);
+  } else {
+    if ((int)blockIdx.x >= tiles) return;
+    tm = (int)blockIdx.x / tiles_n;
+    tn = (int)blockIdx.x % tiles_n;
+  }
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c32 = lane & 31;
+  const int NBT = g.N / 32;
+  const int nbw0 = tn * 8 + wave * 2;
+  const int m0 = tm * MW;
+  const int KS = g.K / 64;
+  const int ks0 = blockIdx.z * g.ksteps_per_split;
+  const int nk = min(KS, ks0 + g.ksteps_per_split) - ks0;
+  const bool nbv[2] = {nbw0 < NBT, nbw0 + 1 < NBT};
+  // Out-of-range column blocks load a valid block (results are not stored).
+  const int nbl[2] = {min(nbw0, NBT - 1), min(nbw0 + 1, NBT - 1)};
+
+  // Chunk c = tid + 256 i of the A tile: row c/8, k-chunk c%8, stored
+  // XOR-swizzled. Rows past M load row M-1 (their results are not stored).
+  // (Element offsets fit 32 bits: the host checks M*K.) Chunk i sits 256
+  // slots after chunk i-1 in the swizzled tile.
+  uint32_t aoff[ACH];
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++) {
+  for (int i = 0; i < ACH; i++) {
+    const int row = (tid >> 3) + 32 * i;
+    aoff[i] = (uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)((tid & 7) * 8);
+  }
+  const int aphys0 = a_slot(tid >> 3, tid & 7);
+  const half_t* xa = (const half_t*)g.x;
+  u32x4_t ra[ACH];
+  BRaw<FORM> bq[4][2];  // B(k) in slot k % 4; three are live at a time
+  // (No lambdas over ra/bq here: a closure holding their addresses would keep
+  // them in scratch memory across the scheduling barrier below.)
+#define PIPE_LOAD_A(ks)                                                              \
+  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
+      ra[i] = *(const u32x4_t*)(xa + aoff[i] + (uint32_t)(ks) * 64u)
+#define PIPE_STORE_A(stage)                                                          \
+  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
+      ((u32x4_t*)As[stage])[aphys0 + 256 * i] = ra[i]
+
+  float16_t acc[MB][2];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = m0 + mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (row >= g.M) continue;
-      if (split) {
-        float* dst = g.part + ((size_t)blockIdx.z * g.M + row) * g.N;
+  for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
-          if (nbv[b]) dst[(nbw0 + b) * 32 + c32] = acc[mb][b][r];
-      } else if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
-        if (nbv[1]) {
-          const float v = silu_f(acc[mb][0][r]) * acc[mb][1][r];
-          const int col = (nbw0 >> 1) * 32 + c32;
-          const size_t o = (size_t)row * (g.N / 2) + col;
-          if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[o] = (half_t)v;
-          else ((float*)g.y)[o] = v;
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
+
+  auto kpos = [&](int k) { return ks0 + k; };
+  if (nk > 0) {
+    const int k1 = kpos(min(1, nk - 1));
+    PIPE_LOAD_A(kpos(0));
+#pragma unroll
+    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(0), lane, bq[0][b]);
+#pragma unroll
+    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], k1, lane, bq[1][b]);
+    PIPE_STORE_A(0);
+  }
+  // nk is a multiple of 4 (the host guarantees it), so the unrolled body has
+  // no conditionals and the loop carries its loads across the back edge.
+  for (int kk = 0; kk < nk; kk += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      {
+        // LDS stage u%2 holds A(k); stage (u+1)%2 is no longer read.
+        lds_barrier();
+        PIPE_LOAD_A(kpos(min(kk + u + 1, nk - 1)));
+        const int kn = kpos(min(kk + u + 2, nk - 1));
+#pragma unroll
+        for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kn, lane, bq[(u + 2) % 4][b]);
+        // Keep the loads issued here, ahead of the MFMAs: the scheduler would
+        // otherwise sink them next to their use and expose their latency.
+        __builtin_amdgcn_sched_barrier(0);
+        const half8_t* A = (const half8_t*)As[u % 2];
+        // Substep j's MFMAs run while substep j+1's A fragments are read from
+        // LDS and its B fragments dequantized; the group barriers interleave
+        // them (1 MFMA, 1 LDS read, 5 VALU) so the matrix core stays fed.
+        half8_t afc[MB], afn[MB], bfc[2], bfn[2];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
+#pragma unroll
+        for (int b = 0; b < 2; b++) bfc[b] = bfrag(bq[u % 4][b], 0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (j < 3) {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) afn[mb] = A[a_slot(mb * 32 + c32, 2 * (j + 1) + h)];
+#pragma unroll
+            for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[u % 4][b], j + 1);
+          }
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
+          if (j < 3) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+              __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            }
+          }
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++) afc[mb] = afn[mb];
+#pragma unroll
+          for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
         }
-      } else {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-          if (!nbv[b]) continue;
-          const size_t o = (size_t)row * g.N + (nbw0 + b) * 32 + c32;
-          if (EPI == EPI_F32) ((float*)g.y)[o] = acc[mb][b][r];
-          else if (EPI == EPI_F16) ((half_t*)g.y)[o] = (half_t)acc[mb][b][r];
-          else ((float*)g.y)[o] += acc[mb][b][r];
-        }
+        // The next A tile goes to LDS only after this step's MFMAs have been
+        // issued, so its global load had the whole step to arrive.
+        __builtin_amdgcn_sched_barrier(0);
+        PIPE_STORE_A((u + 1) % 2);
       }
     }
   }
+  gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, gridDim.z > 1, blockIdx.z);
+#undef PIPE_LOAD_A
+#undef PIPE_STORE_A
 }
 
 // Sums split-K partials in split order and applies the epilogue.
@@ -571,16 +741,111 @@ static void launch_mw(int form, const GemmArgs& g, int epi, dim3 grid, hipStream
   }
 }
 
+static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st) {
+  const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? g.N / 2 : g.N;
+  const size_t total = (size_t)g.M * outN;
+  const dim3 rg((unsigned)((total + 255) / 256)), rb(256);
+  switch (epi) {
+    case EPI_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F32>, rg, rb, 0, st, g, splits); break;
+    case EPI_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F16>, rg, rb, 0, st, g, splits); break;
+    case EPI_RESID: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RESID>, rg, rb, 0, st, g, splits); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F16>, rg, rb, 0, st, g, splits); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F32>, rg, rb, 0, st, g, splits); break;
+  }
+}
+
+// Split-K factor for the pipelined kernel: none when the tiles fill at least
+// half the chip's slots (2 per CU); otherwise as many splits as fit in one
+// round of slots, keeping >= 8 k-steps per split.
+static int choose_pipe_splits(int tiles, int KS, int ncu) {
+  const int slots = 2 * ncu;
+  if (tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
+  int s = slots / tiles;              // one round of workgroups
+  while (s > 1 && KS / s < 8) s--;
+  return std::max(1, std::min(s, 8));
+}
+
+static void pipe_shape(const PackedWeight& w, int M, int ncu, int& tiles_n, int& tiles, int& splits) {
+  tiles_n = (w.N / 32 + 7) / 8;
+  tiles = tiles_n * ((M + 127) / 128);
+  splits = choose_pipe_splits(tiles, w.K / 64, ncu);
+}
+
 // Workspace bytes a call needs for split-K partials.
 size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
-  const int s = choose_splits(M, w.N, w.K, MW, ncu);
+  int s = choose_splits(M, w.N, w.K, MW, ncu);
+  int tiles_n, tiles, ps;
+  pipe_shape(w, M, ncu, tiles_n, tiles, ps);
+  s = std::max(s, ps);
   return s > 1 ? (size_t)s * M * w.N * sizeof(float) : 0;
+}
+
+template <int FORM>
+static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
+                             hipStream_t st) {
+  const dim3 blk(256);
+  switch (epi) {
+    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32>), grid, blk, 0, st, g, tiles_n, tiles); break;
+  }
+}
+
+static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
+                             float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
+  int tiles_n, tiles, splits;
+  pipe_shape(w, M, ncu, tiles_n, tiles, splits);
+  GemmArgs g{};
+  g.x = x;
+  g.wp = w.wp;
+  g.ws = w.ws;
+  g.wz = w.wz;
+  g.y = y;
+  g.M = M;
+  g.K = w.K;
+  g.N = w.N;
+  const int KS = w.K / 64;
+  // whole groups of 4 k-steps per split (KS is a multiple of 4)
+  g.ksteps_per_split = ((KS + splits - 1) / splits + 3) / 4 * 4;
+  splits = (KS + g.ksteps_per_split - 1) / g.ksteps_per_split;
+  if (splits > 1) {
+    if (!workspace || ws_bytes < (size_t)splits * M * w.N * sizeof(float))
+      return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
+    g.part = workspace;
+  }
+  static const int map = [] { const char* e = getenv("TGOHIP_GEMM_MAP"); return e ? atoi(e) : 0; }();
+  g.map = map;
+  const dim3 grid((unsigned)(map == 0 ? 8 * ((tiles_n + 7) / 8) * (tiles / tiles_n) : tiles), 1,
+                  (unsigned)splits);
+  launch_pipe_form<TGOHIP_FORM_I4_SYM>(g, epi, grid, tiles_n, tiles, st);
+  if (splits > 1) launch_reduce(g, epi, splits, st);
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+// The pipelined kernel serves f16 activations from this many rows up.
+static int pipe_min_rows() {
+  static const int v = [] {
+    const char* e = getenv("TGOHIP_GEMM_PIPE_MIN");
+    return e ? atoi(e) : 96;
+  }();
+  return v;
+}
+
+// The pipelined kernel's register ring fits the int4-sym pack; other forms and
+// f32 activations use gemm_kernel.
+static bool use_pipe(const PackedWeight& w, bool x_f32, int M) {
+  return !x_f32 && w.form == TGOHIP_FORM_I4_SYM && M >= pipe_min_rows() && (w.K / 64) % 4 == 0 &&
+         (int64_t)M * w.K < ((int64_t)1 << 31);  // its activation offsets are 32-bit
 }
 
 int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
                  float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
   if (M <= 0) return 0;
+  if (use_pipe(w, x_f32, M)) return gemm_pipe_enqueue(w, x, M, y, epi, workspace, ws_bytes, ncu, st);
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   const int splits = choose_splits(M, w.N, w.K, MW, ncu);
   GemmArgs g{};
@@ -610,18 +875,7 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
     if (x_f32) launch_mw<128, true>(w.form, g, epi, grid, st);
     else launch_mw<128, false>(w.form, g, epi, grid, st);
   }
-  if (splits > 1) {
-    const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? w.N / 2 : w.N;
-    const size_t total = (size_t)M * outN;
-    const dim3 rg((unsigned)((total + 255) / 256)), rb(256);
-    switch (epi) {
-      case EPI_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F32>, rg, rb, 0, st, g, splits); break;
-      case EPI_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F16>, rg, rb, 0, st, g, splits); break;
-      case EPI_RESID: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RESID>, rg, rb, 0, st, g, splits); break;
-      case EPI_SWIGLU_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F16>, rg, rb, 0, st, g, splits); break;
-      case EPI_SWIGLU_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F32>, rg, rb, 0, st, g, splits); break;
-    }
-  }
+  if (splits > 1) launch_reduce(g, epi, splits, st);
   TGOHIP_HIP(hipGetLastError());
   return 0;
 }
