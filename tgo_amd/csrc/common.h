@@ -40,7 +40,8 @@ struct AttnItem {
   int32_t kv_lo;
   int32_t kv_hi;
   int32_t part;  // partial slot for a split item, -1 when the item writes `out`
-  int32_t mode;  // 0: rows <= 16, the four waves split the positions; 1: waves split rows
+  int32_t mode;  // 0: rows <= 16, the four waves split the positions; 1: waves split rows;
+                 // 2: an empty slot of the launch order
 };
 // One combine item: merges nparts partial results of a (sequence, kv head, tokens).
 struct AttnCombine {
@@ -55,7 +56,7 @@ struct AttnCombine {
 
 constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
 constexpr int kAttnSplit = 1024;  // positions per part of a context-split item
-constexpr int kAttnRowsP = 64;    // rows per prefill-style item (4 waves x 16)
+constexpr int kAttnRowsP = 128;   // rows per prefill-style item (4 waves x 32)
 constexpr int kHeadDim = 128;
 
 struct AttnPlan {

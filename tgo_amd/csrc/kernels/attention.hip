@@ -73,305 +73,483 @@ __device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const
   }
 }
 
-constexpr int kVtStride = kAttnTile + 4;  // halves per transposed-V row (bank spread)
+constexpr int kVtStride = kAttnTile + 8;  // halves per transposed-V row (bank spread)
 constexpr int kMaxItemPages = 1024;        // page indices an item stages in LDS
+constexpr int kAttnSmem = 16384 + 128 * kVtStride * 2 + kMaxItemPages * 4;
 
-// BLK is the page size when it is 16 (the fast path: a 64-position tile is
-// four whole pages), or 0 for any other page size.
+// Offset (halves) of transposed-V element (dim row, position c), c a multiple
+// of 4. Groups of 4 positions are XOR-swizzled by 9*(row/16) so the
+// transposing stores (16 lanes on rows 8 apart) and the MFMA operand reads (16
+// or 32 consecutive rows) all spread over the 64 banks.
+__device__ __forceinline__ int vt_off(int row, int c) {
+  return row * kVtStride + ((((c >> 2) ^ (((row >> 4) * 9) & 15))) << 2);
+}
+
+// A workgroup barrier that orders LDS only: global loads in flight stay in
+// flight across it (__syncthreads would wait for them).
+__device__ __forceinline__ void attn_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// What every work item shares: where its sequence, pages and tiles are.
+struct AttnCtx {
+  int s, kvh, G, L, n, cu;
+  int blk, bshift;
+  bool pow2, staged;
+  int pg0;
+  uint32_t rstride;          // elements per pool row (Hkv * 128)
+  const uint32_t* prow;      // the sequence's page-table row
+  const uint32_t* pg;        // staged page indices (LDS)
+  uint32_t lane_off;         // this thread's element offset inside a pool row
+  int dch, pgrp;             // this thread's 16-byte chunk and position group
+};
+
+__device__ __forceinline__ uint32_t attn_row_of(const AttnCtx& c, int p) {
+  const int pi = c.pow2 ? (p >> c.bshift) : (p / c.blk);
+  const int po = c.pow2 ? (p & (c.blk - 1)) : (p - pi * c.blk);
+  const uint32_t page = c.staged ? c.pg[pi - c.pg0] : c.prow[pi];
+  return page * (uint32_t)c.blk + (uint32_t)po;
+}
+
+// Loads one 64-position tile into registers: K chunks of positions
+// pgrp + 16i, V chunks of the four consecutive positions 4*pgrp + i, dims
+// 8*dch + [0,8). Positions at or past hi load zeros.
 template <int BLK>
-__global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs a) {
-  // Ks: 64 positions x 128 dims, 16-byte chunks XOR-swizzled by position.
-  // Vt: V transposed, 128 dims x 64 positions (+4 pad): the PV A operand is
-  // then one 8-byte read. pg: the item's page indices.
-  __shared__ __attribute__((aligned(16))) char smem[16384 + 128 * kVtStride * 2 + kMaxItemPages * 4];
+__device__ __forceinline__ void attn_load_tile(const AttnArgs& a, const AttnCtx& c, int t0, int hi,
+                                               uint4 (&kr)[4], uint4 (&vr)[4]) {
+  if (BLK == 16 && c.staged && t0 + kAttnTile <= hi && (t0 & 15) == 0) {
+    // four whole pages: page i holds K positions t0+16i+pgrp; V's four
+    // consecutive positions all sit in page pgrp/4
+    const int pb = (t0 >> 4) - c.pg0;
+    const uint32_t vrow = c.pg[pb + (c.pgrp >> 2)] * 16u + (uint32_t)(4 * (c.pgrp & 3));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t krow = c.pg[pb + i] * 16u + (uint32_t)c.pgrp;
+      kr[i] = *(const uint4*)(a.k + krow * c.rstride + c.lane_off);
+      vr[i] = *(const uint4*)(a.v + (vrow + i) * c.rstride + c.lane_off);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int pk = t0 + c.pgrp + 16 * i, pv = t0 + 4 * c.pgrp + i;
+    kr[i] = pk < hi ? *(const uint4*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+                    : make_uint4(0, 0, 0, 0);
+    vr[i] = pv < hi ? *(const uint4*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+                    : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Writes a loaded tile to LDS: K row-major (one 256-byte bank row per
+// position, 16-byte chunks XOR-swizzled by position), V transposed.
+__device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, half_t* Vt,
+                                                const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int pos = c.pgrp + 16 * i;
+    ((uint4*)Ks)[pos * 16 + (c.dch ^ (pos & 15))] = kr[i];
+  }
+  union U { uint4 u; half8_t h; };
+  U v0, v1, v2, v3;
+  v0.u = vr[0]; v1.u = vr[1]; v2.u = vr[2]; v3.u = vr[3];
+#pragma unroll
+  for (int d = 0; d < 8; d++) {
+    const half4_t col = {v0.h[d], v1.h[d], v2.h[d], v3.h[d]};
+    *(half4_t*)(Vt + vt_off(c.dch * 8 + d, 4 * c.pgrp)) = col;
+  }
+}
+
+// q (f32 or f16) times scale*log2(e), split into an f16 high and low part.
+__device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool valid, half8_t& hi,
+                                            half8_t& lo) {
+  float x[8];
+  if (valid) {
+    if (a.q_f16) {
+      const half8_t h = *(const half8_t*)((const half_t*)a.q + off);
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] = (float)h[j];
+    } else {
+      const float4_t u = *(const float4_t*)((const float*)a.q + off);
+      const float4_t w = *(const float4_t*)((const float*)a.q + off + 4);
+      x[0] = u[0]; x[1] = u[1]; x[2] = u[2]; x[3] = u[3];
+      x[4] = w[0]; x[5] = w[1]; x[6] = w[2]; x[7] = w[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; j++) x[j] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float xs = x[j] * a.qscale;
+    const half_t h = (half_t)xs;
+    hi[j] = h;
+    lo[j] = (half_t)(xs - (float)h);
+  }
+}
+
+// Decode-style item (at most 16 rows: the G query heads of <= 16/G tokens).
+// The four waves take the four 16-position blocks of each 64-position tile and
+// merge their softmax states at the end. Two tiles of loads are in flight.
+template <int BLK>
+__device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
+                                            char* smem) {
   half_t* Ks = (half_t*)smem;
   half_t* Vt = (half_t*)(smem + 16384);
-  uint32_t* pg = (uint32_t*)(smem + 16384 + 128 * kVtStride * 2);
-
-  const AttnItem it = a.items[blockIdx.x];
-  if (it.mode == 2) return;  // an empty slot of the XCD-aware order
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int s = it.seq, kvh = it.kvh, G = a.G;
-  const int L = (int)a.lengths[s], n = (int)a.extents[s], cu = a.cu[s];
-  const int R = it.ntok * G;
-  const bool pmode = it.mode == 1;
-  const int r = (pmode ? wave * 16 : 0) + li;
+  const int G = c.G, R = it.ntok * G;
+  const int r = li;
   const bool valid = r < R;
   const int tok = it.tok0 + (valid ? r / G : 0);
-  const int head = kvh * G + (valid ? r % G : 0);
-  const int lim = valid ? (L - n + tok) : -1;
-  const int blk = BLK ? BLK : a.block;
-  const bool pow2 = (blk & (blk - 1)) == 0;
-  const int bshift = pow2 ? __ffs(blk) - 1 : 0;
-  // Element offsets of one layer's pool fit 32 bits (the host checks).
-  const uint32_t rstride = (uint32_t)a.Hkv * kHeadDim;
+  const int head = c.kvh * G + (valid ? r % G : 0);
+  const int lim = valid ? (c.L - c.n + tok) : -1;
 
-  // The item's page indices, staged once (a decode part spans <= 33 pages).
-  const uint32_t* prow = a.pages + (size_t)s * a.max_pages;
-  const int pg0 = it.kv_lo / blk;
-  const int npg = it.kv_hi > it.kv_lo ? (it.kv_hi - 1) / blk - pg0 + 1 : 0;
-  const bool staged = npg <= kMaxItemPages;
-  if (staged)
-    for (int i = tid; i < npg; i += 256) pg[i] = prow[pg0 + i];
-
-  // Q as the B operand of S^T = K.Q^T, scaled by scale*log2(e), hi + lo.
+  // Q as the B operand of S^T = K.Q^T (v_mfma_f32_16x16x32_f16): lane (li, lg)
+  // holds dims 32c + 8lg + [0,8) of row li.
   half8_t qh[4], ql[4];
   {
-    const size_t qoff = ((size_t)(cu + tok) * a.H + head) * kHeadDim;
+    const size_t qoff = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      float x[8];
-      const int d0 = 32 * c + 8 * lg;
-      if (valid) {
-        if (a.q_f16) {
-          half8_t h = *(const half8_t*)((const half_t*)a.q + qoff + d0);
-#pragma unroll
-          for (int j = 0; j < 8; j++) x[j] = (float)h[j];
-        } else {
-          float4_t u = *(const float4_t*)((const float*)a.q + qoff + d0);
-          float4_t w = *(const float4_t*)((const float*)a.q + qoff + d0 + 4);
-          x[0] = u[0]; x[1] = u[1]; x[2] = u[2]; x[3] = u[3];
-          x[4] = w[0]; x[5] = w[1]; x[6] = w[2]; x[7] = w[3];
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) x[j] = 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float xs = x[j] * a.qscale;
-        const half_t hi = (half_t)xs;
-        qh[c][j] = hi;
-        ql[c][j] = (half_t)(xs - (float)hi);
-      }
-    }
+    for (int cc = 0; cc < 4; cc++) attn_load_q(a, qoff + 32 * cc + 8 * lg, valid, qh[cc], ql[cc]);
   }
-  __syncthreads();  // pg visible
 
   float m = -INFINITY, l = 0.f;
   float4_t o[8];
 #pragma unroll
   for (int db = 0; db < 8; db++) o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int full_hi = min(it.kv_hi, c.L - c.n + it.tok0 + 1);
 
-  auto row_of = [&](int p) -> uint32_t {
-    const int pi = pow2 ? (p >> bshift) : (p / blk);
-    const int po = pow2 ? (p & (blk - 1)) : (p - pi * blk);
-    const uint32_t page = staged ? pg[pi - pg0] : prow[pi];
-    return page * (uint32_t)blk + (uint32_t)po;
-  };
-  // Per tile a thread moves K chunks of positions tid/16 + 16i and V chunks of
-  // the four consecutive positions 4*(tid/16) + i, dims 8*(tid%16) + [0,8).
-  const int dch = tid & 15, pgrp = tid >> 4;
-  const uint32_t lane_off = (uint32_t)kvh * kHeadDim + dch * 8;
-  uint4 kreg[4], vreg[4];
-  auto load_tile = [&](int t0) {
-    if (BLK == 16 && staged && t0 + kAttnTile <= it.kv_hi && (t0 & 15) == 0) {
-      // four whole pages: page i holds K positions t0+16i+pgrp; V's four
-      // consecutive positions all sit in page pgrp/4
-      const int pb = (t0 >> 4) - pg0;
-      const uint32_t vrow = pg[pb + (pgrp >> 2)] * 16u + (uint32_t)(4 * (pgrp & 3));
+  uint4 kr[2][4], vr[2][4];
+  if (it.kv_lo < it.kv_hi) attn_load_tile<BLK>(a, c, it.kv_lo, it.kv_hi, kr[0], vr[0]);
+  if (it.kv_lo + kAttnTile < it.kv_hi)
+    attn_load_tile<BLK>(a, c, it.kv_lo + kAttnTile, it.kv_hi, kr[1], vr[1]);
+  for (int tt = it.kv_lo; tt < it.kv_hi; tt += 2 * kAttnTile) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t krow = pg[pb + i] * 16u + (uint32_t)pgrp;
-        kreg[i] = *(const uint4*)(a.k + krow * rstride + lane_off);
-        vreg[i] = *(const uint4*)(a.v + (vrow + i) * rstride + lane_off);
-      }
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int pk = t0 + pgrp + 16 * i, pv = t0 + 4 * pgrp + i;
-      if (pk < it.kv_hi) kreg[i] = *(const uint4*)(a.k + row_of(pk) * rstride + lane_off);
-      else kreg[i] = make_uint4(0, 0, 0, 0);
-      if (pv < it.kv_hi) vreg[i] = *(const uint4*)(a.v + row_of(pv) * rstride + lane_off);
-      else vreg[i] = make_uint4(0, 0, 0, 0);
-    }
-  };
-  // Positions every row of this item may see: the first token's limit.
-  const int full_hi = min(it.kv_hi, L - n + it.tok0 + 1);
+    for (int u = 0; u < 2; u++) {
+      const int t0 = tt + u * kAttnTile;
+      if (t0 < it.kv_hi) {
+        attn_lds_barrier();  // the previous tile's LDS reads are done
+        attn_store_tile(c, Ks, Vt, kr[u], vr[u]);
+        attn_lds_barrier();
+        if (t0 + 2 * kAttnTile < it.kv_hi)
+          attn_load_tile<BLK>(a, c, t0 + 2 * kAttnTile, it.kv_hi, kr[u], vr[u]);
 
-  int t0 = it.kv_lo;
-  if (t0 < it.kv_hi) load_tile(t0);
-  for (; t0 < it.kv_hi; t0 += kAttnTile) {
-    __syncthreads();
+        // Scores of this wave's 16-position block.
+        const int mb = wave;
+        float4_t st = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (t0 + mb * 16 < it.kv_hi) {
+          float4_t acc = {0.f, 0.f, 0.f, 0.f};
+          const int pos = mb * 16 + li;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int pos = pgrp + 16 * i;
-      ((uint4*)Ks)[pos * 16 + (dch ^ (pos & 15))] = kreg[i];
-    }
-    {
-      union U { uint4 u; half8_t h; };
-      U v0, v1, v2, v3;
-      v0.u = vreg[0]; v1.u = vreg[1]; v2.u = vreg[2]; v3.u = vreg[3];
+          for (int cc = 0; cc < 4; cc++) {
+            const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((4 * cc + lg) ^ (pos & 15))) * 8);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[cc], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[cc], acc, 0, 0, 0);
+          }
+          if (t0 + mb * 16 + 16 <= full_hi && valid) {
+            st = acc;
+          } else {
 #pragma unroll
-      for (int d = 0; d < 8; d++) {
-        const half4_t col = {v0.h[d], v1.h[d], v2.h[d], v3.h[d]};
-        *(half4_t*)(Vt + (dch * 8 + d) * kVtStride + 4 * pgrp) = col;
-      }
-    }
-    __syncthreads();
-    if (t0 + kAttnTile < it.kv_hi) load_tile(t0 + kAttnTile);
-
-    // Scores for this wave's 16-position blocks of the tile: decode-style items
-    // take block `wave`, prefill-style items all four.
-    const int mb0 = pmode ? 0 : wave, nmb = pmode ? 4 : 1;
-    float4_t st[4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      st[j] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-      if (j >= nmb) continue;
-      const int mb = mb0 + j;
-      if (t0 + mb * 16 >= it.kv_hi) continue;
-      float4_t acc = {0.f, 0.f, 0.f, 0.f};
-      const int pos = mb * 16 + li;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((4 * c + lg) ^ (pos & 15))) * 8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[c], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], acc, 0, 0, 0);
-      }
-      if (t0 + mb * 16 + 16 <= full_hi && valid) {
+            for (int q = 0; q < 4; q++) {
+              const int pabs = t0 + mb * 16 + 4 * lg + q;
+              st[q] = (pabs <= lim && pabs < it.kv_hi) ? acc[q] : -INFINITY;
+            }
+          }
+        }
+        float tmax = fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3]));
+        tmax = wave_max16x(tmax);
+        // Branch-free update: a row that has seen no visible position keeps
+        // m = -inf, alpha = 1 and p = 0. The MFMAs below run on every lane.
+        const float mnew = fmaxf(m, tmax);
+        const bool none = mnew == -INFINITY;
+        const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+        float psum = 0.f;
+        half4_t pb;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          st[j][q] = acc[q];
-          tmax = fmaxf(tmax, acc[q]);
+          const float p = none ? 0.f : __builtin_amdgcn_exp2f(st[q] - mnew);
+          psum += p;
+          pb[q] = (half_t)p;
         }
-      } else {
+        psum = wave_sum16x(psum);
+        l = l * alpha + psum;
+        m = mnew;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int pabs = t0 + mb * 16 + 4 * lg + q;
-          st[j][q] = (pabs <= lim && pabs < it.kv_hi) ? acc[q] : -INFINITY;
-          tmax = fmaxf(tmax, st[j][q]);
+        for (int db = 0; db < 8; db++) o[db] *= alpha;
+        if (t0 + mb * 16 < it.kv_hi) {
+          // O^T += V^T . P^T; the A operand is V^T[dim 16db+li][pos 16mb+4lg..+3].
+#pragma unroll
+          for (int db = 0; db < 8; db++) {
+            const half4_t va = *(const half4_t*)(Vt + vt_off(db * 16 + li, mb * 16 + 4 * lg));
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[db], 0, 0, 0);
+          }
         }
-      }
-    }
-    tmax = wave_max16x(tmax);
-    // Branch-free update: a row that has seen no visible position keeps
-    // m = -inf, alpha = 1 and p = 0. The MFMAs below must run on every lane
-    // (a lane's A operand is a head dimension, not this lane's row).
-    const float mnew = fmaxf(m, tmax);
-    const bool none = mnew == -INFINITY;
-    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
-    float psum = 0.f;
-    half4_t pb[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float p = none ? 0.f : __builtin_amdgcn_exp2f(st[j][q] - mnew);
-        psum += p;
-        pb[j][q] = (half_t)p;
-      }
-    psum = wave_sum16x(psum);
-    l = l * alpha + psum;
-    m = mnew;
-#pragma unroll
-    for (int db = 0; db < 8; db++) o[db] *= alpha;
-    // O^T += V^T . P^T; the A operand is V^T[dim 16db+li][pos 16mb+4lg..+3].
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if (j >= nmb) break;
-      const int mb = mb0 + j;
-      if (t0 + mb * 16 >= it.kv_hi) break;
-#pragma unroll
-      for (int db = 0; db < 8; db++) {
-        const half4_t va = *(const half4_t*)(Vt + (db * 16 + li) * kVtStride + mb * 16 + 4 * lg);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb[j], o[db], 0, 0, 0);
       }
     }
   }
 
-  if (!pmode) {
-    // Merge the four waves' partial softmax states for the (up to) 16 rows.
-    __syncthreads();
-    float* Os = (float*)smem;               // [4][16][128]
-    float* Ms = (float*)(smem + 32768);     // [4][16] m, then [4][16] l
+  // Merge the four waves' partial softmax states for the (up to) 16 rows.
+  attn_lds_barrier();
+  // Os rows are padded to 132 floats so the 16 rows a store instruction
+  // touches land on distinct banks.
+  constexpr int kOs = 132;
+  float* Os = (float*)smem;                        // [4][16][kOs]
+  float* Ms = (float*)(smem + 4 * 16 * kOs * 4);   // [4][16] m, then [4][16] l
 #pragma unroll
-    for (int db = 0; db < 8; db++)
+  for (int db = 0; db < 8; db++) *(float4_t*)(Os + (wave * 16 + li) * kOs + db * 16 + 4 * lg) = o[db];
+  if (lg == 0) {
+    Ms[wave * 16 + li] = m;
+    Ms[64 + wave * 16 + li] = l;
+  }
+  attn_lds_barrier();
+  const int row = tid >> 4, d0 = (tid & 15) * 8;
+  float mstar = -INFINITY;
 #pragma unroll
-      for (int q = 0; q < 4; q++) Os[(wave * 16 + li) * 128 + db * 16 + 4 * lg + q] = o[db][q];
-    if (lg == 0) {
-      Ms[wave * 16 + li] = m;
-      Ms[64 + wave * 16 + li] = l;
-    }
-    __syncthreads();
-    const int row = tid >> 4, d0 = (tid & 15) * 8;
-    float mstar = -INFINITY;
+  for (int w = 0; w < 4; w++) mstar = fmaxf(mstar, Ms[w * 16 + row]);
+  float lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int w = 0; w < 4; w++) mstar = fmaxf(mstar, Ms[w * 16 + row]);
-    float lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int w = 0; w < 4; w++) {
+    const float mw = Ms[w * 16 + row];
+    const float wt = (mw == -INFINITY) ? 0.f : exp2f(mw - mstar);
+    lsum += wt * Ms[64 + w * 16 + row];
+    const float* src = Os + (w * 16 + row) * kOs + d0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      const float mw = Ms[w * 16 + row];
-      const float wt = (mw == -INFINITY) ? 0.f : exp2f(mw - mstar);
-      lsum += wt * Ms[64 + w * 16 + row];
-      const float* src = Os + (w * 16 + row) * 128 + d0;
+    for (int j = 0; j < 8; j++) acc[j] += wt * src[j];
+  }
+  if (row < R) {
+    if (it.part < 0) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc[j] += wt * src[j];
-    }
-    if (row < R) {
-      if (it.part < 0) {
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      for (int j = 0; j < 8; j++) acc[j] *= inv;
+      const int tk = it.tok0 + row / G, hd = c.kvh * G + row % G;
+      store_out8(a.out, a.out_f16, ((size_t)(c.cu + tk) * a.H + hd) * kHeadDim + d0, acc);
+    } else {
+      float* po = a.part_o + ((size_t)it.part * kAttnRowsP + row) * 128 + d0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[j] *= inv;
-        const int tk = it.tok0 + row / G, hd = kvh * G + row % G;
-        store_out8(a.out, a.out_f16, ((size_t)(cu + tk) * a.H + hd) * kHeadDim + d0, acc);
-      } else {
-        float* po = a.part_o + ((size_t)it.part * 64 + row) * 128 + d0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) po[j] = acc[j];
-        if ((tid & 15) == 0) {
-          a.part_ml[(size_t)it.part * 128 + row] = mstar;
-          a.part_ml[(size_t)it.part * 128 + 64 + row] = lsum;
-        }
-      }
-    }
-  } else if (valid && it.part >= 0) {
-    // a part of a context-split prefill item: unnormalized O and (m, l)
-    float* po = a.part_o + ((size_t)it.part * 64 + r) * 128;
-#pragma unroll
-    for (int db = 0; db < 8; db++) *(float4_t*)(po + db * 16 + 4 * lg) = o[db];
-    if (lg == 0) {
-      a.part_ml[(size_t)it.part * 128 + r] = m;
-      a.part_ml[(size_t)it.part * 128 + 64 + r] = l;
-    }
-  } else if (valid) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const size_t base = ((size_t)(cu + tok) * a.H + head) * kHeadDim;
-#pragma unroll
-    for (int db = 0; db < 8; db++) {
-      const size_t off = base + db * 16 + 4 * lg;
-      if (a.out_f16) {
-        half4_t hv;
-#pragma unroll
-        for (int q = 0; q < 4; q++) hv[q] = (half_t)(o[db][q] * inv);
-        *(half4_t*)((half_t*)a.out + off) = hv;
-      } else {
-        *(float4_t*)((float*)a.out + off) = o[db] * inv;
+      for (int j = 0; j < 8; j++) po[j] = acc[j];
+      if ((tid & 15) == 0) {
+        a.part_ml[(size_t)it.part * 2 * kAttnRowsP + row] = mstar;
+        a.part_ml[(size_t)it.part * 2 * kAttnRowsP + kAttnRowsP + row] = lsum;
       }
     }
   }
 }
 
-// Merges the parts of split items in part order (deterministic). One block
-// per item; a thread owns 8 dims of a row, 16 rows per pass.
+// Prefill-style item (up to 128 rows = 32 tokens x 4 query heads): wave w owns
+// rows 32w + [0,32) and every wave consumes every staged tile.
+//   S^T = K . Q^T on v_mfma_f32_32x32x16_f16: A = K (32 positions x 16 dims,
+//   lane (p, kh) reads position p, dims 16s + 8kh + [0,8)), B = Q^T from
+//   registers (hi + lo). Lane (r, kh) gets the scores of row r at positions
+//   8(i/4) + 4kh + i%4, i = 0..15, of each 32-position block.
+//   O^T += V^T . P^T on the same MFMA: its k index 8kh + e maps to position
+//   16t + (e < 4 ? 4kh + e : 8 + 4kh + e - 4) of the block, which is exactly
+//   where the lane's own probabilities sit (scores i = 8t..8t+7), so P never
+//   leaves registers; the A operand is two 8-byte reads of transposed V.
+template <int BLK>
+__device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
+                                             char* smem) {
+  half_t* Ks = (half_t*)smem;
+  half_t* Vt = (half_t*)(smem + 16384);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int G = c.G, R = it.ntok * G;
+  const int r = wave * 32 + l32;
+  const bool valid = r < R;
+  const int tok = it.tok0 + (valid ? r / G : 0);
+  const int head = c.kvh * G + (valid ? r % G : 0);
+  const int lim = valid ? (c.L - c.n + tok) : -1;
+  // Positions every valid row of this wave may see (its first token's limit),
+  // and whether the wave's rows are all valid.
+  const int wtok0 = it.tok0 + (wave * 32) / G;
+  const int wave_hi = min(it.kv_hi, c.L - c.n + wtok0 + 1);
+  const bool wave_full = wave * 32 + 32 <= R;
+
+  half8_t qh[8], ql[8];
+  {
+    const size_t qoff = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
+#pragma unroll
+    for (int ss = 0; ss < 8; ss++) attn_load_q(a, qoff + 16 * ss + 8 * kh, valid, qh[ss], ql[ss]);
+  }
+
+  float m = -INFINITY, l = 0.f;
+  float16_t o[4];
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[db][i] = 0.f;
+
+  uint4 kr[4], vr[4];
+  if (it.kv_lo < it.kv_hi) attn_load_tile<BLK>(a, c, it.kv_lo, it.kv_hi, kr, vr);
+  for (int t0 = it.kv_lo; t0 < it.kv_hi; t0 += kAttnTile) {
+    attn_lds_barrier();
+    attn_store_tile(c, Ks, Vt, kr, vr);
+    attn_lds_barrier();
+    if (t0 + kAttnTile < it.kv_hi) attn_load_tile<BLK>(a, c, t0 + kAttnTile, it.kv_hi, kr, vr);
+    float16_t sc[2];
+#pragma unroll
+    for (int pb = 0; pb < 2; pb++) {
+      float16_t acc;
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[i] = 0.f;
+      const int pos = pb * 32 + l32;
+#pragma unroll
+      for (int ss = 0; ss < 8; ss++) {
+        const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((2 * ss + kh) ^ (pos & 15))) * 8);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ss], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[ss], acc, 0, 0, 0);
+      }
+      sc[pb] = acc;
+    }
+    float tmax = -INFINITY;
+    if (wave_full && t0 + kAttnTile <= wave_hi) {
+#pragma unroll
+      for (int pb = 0; pb < 2; pb++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, sc[pb][i]);
+    } else {
+#pragma unroll
+      for (int pb = 0; pb < 2; pb++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const int p = t0 + pb * 32 + 8 * (i >> 2) + 4 * kh + (i & 3);
+          if (!(p <= lim && p < it.kv_hi)) sc[pb][i] = -INFINITY;
+          tmax = fmaxf(tmax, sc[pb][i]);
+        }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m, tmax);
+    const bool none = mnew == -INFINITY;
+    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+    float psum = 0.f;
+    half8_t pf[2][2];
+#pragma unroll
+    for (int pb = 0; pb < 2; pb++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float p = none ? 0.f : __builtin_amdgcn_exp2f(sc[pb][i] - mnew);
+        psum += p;
+        pf[pb][i >> 3][i & 7] = (half_t)p;
+      }
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+    m = mnew;
+#pragma unroll
+    for (int db = 0; db < 4; db++) o[db] *= alpha;
+    // vt_off(32db + l32, 32pb + 16t + 8e + 4kh) written out: the position
+    // group 8pb + 4t + 2e + kh is XORed with 9*(2db + l32/16) mod 16, i.e. with
+    // 2db (bits 1-2) and the lane's 9*(l32/16) (bits 0, 3), so one lane value
+    // serves every read.
+    const int vrow = l32 * kVtStride, vcol = (kh ^ (9 * (l32 >> 4))) << 2;
+#pragma unroll
+    for (int pb = 0; pb < 2; pb++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+          const int k0 = ((8 * pb + 4 * t) ^ (2 * db)) << 2, k1 = ((8 * pb + 4 * t + 2) ^ (2 * db)) << 2;
+          const half_t* vb = Vt + db * 32 * kVtStride;
+          const half4_t v0 = *(const half4_t*)(vb + vrow + (vcol ^ k0));
+          const half4_t v1 = *(const half4_t*)(vb + vrow + (vcol ^ k1));
+          const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[pb][t], o[db], 0, 0, 0);
+        }
+      }
+  }
+
+  if (!valid) return;
+  // Lane (r, kh) holds dims 32db + 8g + 4kh + [0,4) of row r, g = 0..3.
+  if (it.part < 0) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const size_t base = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const size_t off = base + db * 32 + 8 * g + 4 * kh;
+        if (a.out_f16) {
+          half4_t hv;
+#pragma unroll
+          for (int q = 0; q < 4; q++) hv[q] = (half_t)(o[db][4 * g + q] * inv);
+          *(half4_t*)((half_t*)a.out + off) = hv;
+        } else {
+          const float4_t fv = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                               o[db][4 * g + 3] * inv};
+          *(float4_t*)((float*)a.out + off) = fv;
+        }
+      }
+  } else {
+    float* po = a.part_o + ((size_t)it.part * kAttnRowsP + r) * 128;
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float4_t fv = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+        *(float4_t*)(po + db * 32 + 8 * g + 4 * kh) = fv;
+      }
+    if (kh == 0) {
+      a.part_ml[(size_t)it.part * 2 * kAttnRowsP + r] = m;
+      a.part_ml[(size_t)it.part * 2 * kAttnRowsP + kAttnRowsP + r] = l;
+    }
+  }
+}
+
+// BLK is the page size when it is 16 (the fast path: a 64-position tile is
+// four whole pages), or 0 for any other page size.
+template <int BLK>
+__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmem];
+  const AttnItem it = a.items[blockIdx.x];
+  if (it.mode == 2) return;  // an empty slot of the XCD-aware order
+  const int tid = threadIdx.x;
+  AttnCtx c;
+  c.s = it.seq;
+  c.kvh = it.kvh;
+  c.G = a.G;
+  c.L = (int)a.lengths[c.s];
+  c.n = (int)a.extents[c.s];
+  c.cu = a.cu[c.s];
+  c.blk = BLK ? BLK : a.block;
+  c.pow2 = (c.blk & (c.blk - 1)) == 0;
+  c.bshift = c.pow2 ? __ffs(c.blk) - 1 : 0;
+  // Element offsets of one layer's pool fit 32 bits (the host checks).
+  c.rstride = (uint32_t)a.Hkv * kHeadDim;
+  c.prow = a.pages + (size_t)c.s * a.max_pages;
+  uint32_t* pg = (uint32_t*)(smem + 16384 + 128 * kVtStride * 2);
+  c.pg = pg;
+  c.pg0 = it.kv_lo / c.blk;
+  const int npg = it.kv_hi > it.kv_lo ? (it.kv_hi - 1) / c.blk - c.pg0 + 1 : 0;
+  c.staged = npg <= kMaxItemPages;
+  if (c.staged)
+    for (int i = tid; i < npg; i += 256) pg[i] = c.prow[c.pg0 + i];
+  c.dch = tid & 15;
+  c.pgrp = tid >> 4;
+  c.lane_off = (uint32_t)c.kvh * kHeadDim + c.dch * 8;
+  __syncthreads();  // pg visible
+  if (it.mode == 0) attn_decode<BLK>(a, it, c, smem);
+  else attn_prefill<BLK>(a, it, c, smem);
+}
+
+// Merges the parts of split items in part order (deterministic). A block
+// takes 16 rows of an item; a thread owns 8 dims of a row.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const AttnCombine cb = a.combines[blockIdx.x];
   const int tid = threadIdx.x, d0 = (tid & 15) * 8, G = a.G;
   const int R = cb.ntok * G;
-  for (int row = tid >> 4; row < R; row += 16) {
+  {
+    const int row = (int)blockIdx.y * 16 + (tid >> 4);  // 16 rows per block
+    if (row >= R) return;
     float mstar = -INFINITY;
     for (int p = 0; p < cb.nparts; p++)
-      mstar = fmaxf(mstar, a.part_ml[(size_t)(cb.part0 + p) * 128 + row]);
+      mstar = fmaxf(mstar, a.part_ml[(size_t)(cb.part0 + p) * 2 * kAttnRowsP + row]);
     float lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int p = 0; p < cb.nparts; p++) {
       const size_t part = (size_t)(cb.part0 + p);
-      const float mw = a.part_ml[part * 128 + row];
+      const float mw = a.part_ml[part * 2 * kAttnRowsP + row];
       const float wt = (mw == -INFINITY) ? 0.f : exp2f(mw - mstar);
-      lsum += wt * a.part_ml[part * 128 + 64 + row];
-      const float* src = a.part_o + (part * 64 + row) * 128 + d0;
+      lsum += wt * a.part_ml[part * 2 * kAttnRowsP + kAttnRowsP + row];
+      const float* src = a.part_o + (part * kAttnRowsP + row) * 128 + d0;
 #pragma unroll
       for (int j = 0; j < 8; j++) acc[j] += wt * src[j];
     }
@@ -490,53 +668,47 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       }
     }
   }
-  // Heavy items first so the tail of the launch is short ones.
-  std::stable_sort(plan.items.begin(), plan.items.end(), [](const AttnItem& x, const AttnItem& y) {
-    const int64_t cx = (int64_t)(x.kv_hi - x.kv_lo) * (x.mode ? 8 : 1);
-    const int64_t cy = (int64_t)(y.kv_hi - y.kv_lo) * (y.mode ? 8 : 1);
-    return cx > cy;
-  });
-  // XCD-aware order: workgroup i is dispatched to XCD i % 8, and every
-  // prefill-style item of one (sequence, kv head) re-reads the same K/V
-  // stream. Route each such stream to one XCD so its L2 serves the re-reads:
-  // the prefill items are dealt into 8 per-XCD queues by stream, then
-  // interleaved back so that position i belongs to queue i % 8.
+  // Launch order. Decode-style items stream K/V (HBM-bound); prefill-style
+  // items re-read their sequence's K/V many times and are MFMA-bound. They are
+  // interleaved evenly so both kinds run side by side for the whole launch,
+  // each kind heavy-first so the tail is short items. Workgroup i is
+  // dispatched to XCD i % 8, and the prefill items of one (sequence, kv head)
+  // all re-read the same K/V stream: each stream is routed to one XCD (its
+  // items take only that XCD's positions) so that XCD's L2 serves the
+  // re-reads.
   {
     constexpr int kXcd = 8;
-    std::vector<AttnItem> pre, rest;
-    for (const AttnItem& x : plan.items) (x.mode ? pre : rest).push_back(x);
-    if (!pre.empty()) {
-      std::vector<std::vector<AttnItem>> q(kXcd);
-      for (const AttnItem& x : pre) q[(x.seq * 131 + x.kvh) % kXcd].push_back(x);
-      std::vector<AttnItem> out;
-      out.reserve(plan.items.size());
-      size_t taken = 0;
-      std::vector<size_t> at(kXcd, 0);
-      while (taken < pre.size()) {
-        for (int x = 0; x < kXcd; x++) {
-          if (at[x] < q[x].size()) {
-            out.push_back(q[x][at[x]++]);
-            taken++;
-          } else if (taken < pre.size()) {
-            // pad this XCD's turn with a decode item so the others keep their lanes
-            if (!rest.empty()) {
-              out.push_back(rest.back());
-              rest.pop_back();
-            } else {
-              out.push_back(AttnItem{0, 0, 0, 0, 0, 0, -1, 2});  // empty item
-            }
-          }
-        }
+    std::vector<AttnItem> pre, dec;
+    for (const AttnItem& x : plan.items) (x.mode ? pre : dec).push_back(x);
+    auto heavy = [](const AttnItem& x, const AttnItem& y) {
+      return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
+    };
+    std::stable_sort(dec.begin(), dec.end(), heavy);
+    std::vector<std::vector<AttnItem>> q(kXcd);
+    for (const AttnItem& x : pre) q[(x.seq * 131 + x.kvh) % kXcd].push_back(x);
+    for (auto& qq : q) std::stable_sort(qq.begin(), qq.end(), heavy);
+    const size_t total = pre.size() + dec.size();
+    std::vector<AttnItem> out;
+    out.reserve(total + kXcd * 4);
+    std::vector<size_t> at(kXcd, 0);
+    size_t taken_pre = 0, taken_dec = 0;
+    while (taken_pre < pre.size() || taken_dec < dec.size()) {
+      const int x = (int)(out.size() % kXcd);
+      const bool pre_here = at[x] < q[x].size();
+      // the prefill share of the launch so far stays at the overall share
+      const bool want_pre = (double)(taken_pre + 1) * (double)total <=
+                            (double)pre.size() * (double)(out.size() + 1) + 1e-9;
+      if (pre_here && (want_pre || taken_dec == dec.size())) {
+        out.push_back(q[x][at[x]++]);
+        taken_pre++;
+      } else if (taken_dec < dec.size()) {
+        out.push_back(dec[taken_dec++]);
+      } else {
+        out.push_back(AttnItem{0, 0, 0, 0, 0, 0, -1, 2});  // this XCD's queue is empty
       }
-      // trailing empty fillers are not needed
-      while (!out.empty() && out.back().mode == 2) out.pop_back();
-      std::reverse(rest.begin(), rest.end());
-      std::stable_sort(rest.begin(), rest.end(), [](const AttnItem& x, const AttnItem& y) {
-        return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
-      });
-      out.insert(out.end(), rest.begin(), rest.end());
-      plan.items.swap(out);
     }
+    while (!out.empty() && out.back().mode == 2) out.pop_back();
+    plan.items.swap(out);
   }
   return 0;
 }
@@ -572,8 +744,8 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
       hipLaunchKernelGGL(attn_kernel<0>, dim3((unsigned)plan.items.size()), dim3(256), 0, stream, a);
   }
   if (!plan.combines.empty())
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)plan.combines.size()), dim3(256), 0,
-                       stream, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)plan.combines.size(), kAttnRowsP / 16),
+                       dim3(256), 0, stream, a);
   if (plan.claimed < T) {
     const size_t start = (size_t)plan.claimed * H * kHeadDim;
     const size_t count = (size_t)(T - plan.claimed) * H * kHeadDim;

@@ -389,9 +389,9 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
 }
 
 int ensure_attn_parts(tgohip_ctx* c, int parts) {
-  int rc = c->part_o.ensure((size_t)std::max(parts, 1) * 64 * 128 * 4);
+  int rc = c->part_o.ensure((size_t)std::max(parts, 1) * kAttnRowsP * 128 * 4);
   if (rc) return rc;
-  return c->part_ml.ensure((size_t)std::max(parts, 1) * 128 * 4);
+  return c->part_ml.ensure((size_t)std::max(parts, 1) * 2 * kAttnRowsP * 4);
 }
 
 }  // namespace
