@@ -189,9 +189,17 @@ __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool 
   }
 }
 
+// Tiles of loads a decode-style item keeps in flight (its registers are free:
+// the prefill path sets the kernel's register budget).
+#ifndef TGOHIP_DECODE_DEPTH
+#define TGOHIP_DECODE_DEPTH 3
+#endif
+constexpr int kDecodeDepth = TGOHIP_DECODE_DEPTH;
+
 // Decode-style item (at most 16 rows: the G query heads of <= 16/G tokens).
 // The four waves take the four 16-position blocks of each 64-position tile and
-// merge their softmax states at the end. Two tiles of loads are in flight.
+// merge their softmax states at the end. kDecodeDepth tiles of loads are in
+// flight.
 template <int BLK>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                             char* smem) {
@@ -221,20 +229,22 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
   for (int db = 0; db < 8; db++) o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
   const int full_hi = min(it.kv_hi, c.L - c.n + it.tok0 + 1);
 
-  uint4 kr[2][4], vr[2][4];
-  if (it.kv_lo < it.kv_hi) attn_load_tile<BLK>(a, c, it.kv_lo, it.kv_hi, kr[0], vr[0]);
-  if (it.kv_lo + kAttnTile < it.kv_hi)
-    attn_load_tile<BLK>(a, c, it.kv_lo + kAttnTile, it.kv_hi, kr[1], vr[1]);
-  for (int tt = it.kv_lo; tt < it.kv_hi; tt += 2 * kAttnTile) {
+  constexpr int D = kDecodeDepth;
+  uint4 kr[D][4], vr[D][4];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < D; u++)
+    if (it.kv_lo + u * kAttnTile < it.kv_hi)
+      attn_load_tile<BLK>(a, c, it.kv_lo + u * kAttnTile, it.kv_hi, kr[u], vr[u]);
+  for (int tt = it.kv_lo; tt < it.kv_hi; tt += D * kAttnTile) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
       const int t0 = tt + u * kAttnTile;
       if (t0 < it.kv_hi) {
         attn_lds_barrier();  // the previous tile's LDS reads are done
         attn_store_tile(c, Ks, Vt, kr[u], vr[u]);
         attn_lds_barrier();
-        if (t0 + 2 * kAttnTile < it.kv_hi)
-          attn_load_tile<BLK>(a, c, t0 + 2 * kAttnTile, it.kv_hi, kr[u], vr[u]);
+        if (t0 + D * kAttnTile < it.kv_hi)
+          attn_load_tile<BLK>(a, c, t0 + D * kAttnTile, it.kv_hi, kr[u], vr[u]);
 
         // Scores of this wave's 16-position block.
         const int mb = wave;
@@ -618,12 +628,21 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
     return fail(TGOHIP_EINVAL, "attention: the extents sum to " + std::to_string(at) +
                                    " and q has " + std::to_string(T) + " rows");
   plan.claimed = (int)at;
-  // Positions per part of a decode-style item (a multiple of the 64-position
-  // tile); TGOHIP_ATTN_SPLIT overrides it for tuning.
+  // Positions per part of a context-split item (multiples of the 64-position
+  // tile). Decode-style items stream: long parts amortize a workgroup's start
+  // (page staging, first loads) and merge. Prefill-style items are MFMA-bound:
+  // shorter parts spread a chunk's work over more workgroups. Both depend only
+  // on the sequence itself, so a mixed launch decomposes every sequence as it
+  // would alone. TGOHIP_ATTN_SPLIT / TGOHIP_ATTN_PSPLIT override them.
   static const int split = [] {
     const char* e = getenv("TGOHIP_ATTN_SPLIT");
-    const int v = e ? atoi(e) : kAttnSplit;
-    return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplit;
+    const int v = e ? atoi(e) : kAttnSplitDecode;
+    return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplitDecode;
+  }();
+  static const int psplit = [] {
+    const char* e = getenv("TGOHIP_ATTN_PSPLIT");
+    const int v = e ? atoi(e) : kAttnSplitPrefill;
+    return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplitPrefill;
   }();
   for (int s = 0; s < B; s++) {
     const int n = (int)extents[s], L = (int)lengths[s];
@@ -652,14 +671,14 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       for (int t0 = 0; t0 < n; t0 += tpi) {
         const int nt = std::min(tpi, n - t0);
         const int hi = L - n + t0 + nt;
-        const int splits = (hi + split - 1) / split;
+        const int splits = (hi + psplit - 1) / psplit;
         for (int kvh = 0; kvh < Hkv; kvh++) {
           if (splits <= 1) {
             plan.items.push_back(AttnItem{s, kvh, t0, nt, 0, hi, -1, 1});
           } else {
             const int part0 = plan.parts;
             for (int p = 0; p < splits; p++) {
-              const int lo = p * split, h2 = std::min(hi, lo + split);
+              const int lo = p * psplit, h2 = std::min(hi, lo + psplit);
               plan.items.push_back(AttnItem{s, kvh, t0, nt, lo, h2, plan.parts++, 1});
             }
             plan.combines.push_back(AttnCombine{s, kvh, t0, nt, part0, splits, 0, 0});
