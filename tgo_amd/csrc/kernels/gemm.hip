@@ -40,7 +40,6 @@ struct GemmArgs {
   float* part;          // split-K partials [splits][M][N]
   int M, K, N;
   int ksteps_per_split;
-  int map;
 };
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) {
@@ -353,27 +352,19 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 // activations, mostly L2-resident) is issued at step j-1 and written to a
 // double-buffered LDS tile at the end of that step. Barriers order LDS only, so
 // loads stay in flight across them.
-template <int FORM, int EPI>
+template <int FORM, int EPI, int MW>
 __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
-  constexpr int MW = 128, MB = 4;
+  constexpr int MB = MW / 32;
   constexpr int ACH = MW / 32;  // 16-byte A chunks per thread per k-step
   __shared__ __attribute__((aligned(16))) half_t As[2][MW * 64];
 
   // XCD x (workgroup b runs on XCD b % 8) owns the column tiles c = x (mod 8):
   // each weight column tile is streamed into one XCD's L2 and serves every row
   // tile there. Within an XCD the order is row-major over its columns.
-  int tm, tn;
-  if (g.map == 0) {
-    const int x = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
-    const int cols_x = (tiles_n - x + 7) / 8;
-    if (cols_x <= 0 || j >= cols_x * (tiles / tiles_n)) return;
-    tm = j / cols_x;
-    tn = x + 8 * (j - tm * cols_x);
-  } else {
-    if ((int)blockIdx.x >= tiles) return;
-    tm = (int)blockIdx.x / tiles_n;
-    tn = (int)blockIdx.x % tiles_n;
-  }
+  const int x = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+  const int cols_x = (tiles_n - x + 7) / 8;
+  if (cols_x <= 0 || j >= cols_x * (tiles / tiles_n)) return;
+  const int tm = j / cols_x, tn = x + 8 * (j - tm * cols_x);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c32 = lane & 31;
@@ -765,9 +756,17 @@ static int choose_pipe_splits(int tiles, int KS, int ncu) {
   return std::max(1, std::min(s, 8));
 }
 
-static void pipe_shape(const PackedWeight& w, int M, int ncu, int& tiles_n, int& tiles, int& splits) {
+// Row-tile height and split-K of the pipelined kernel. Up to 384 rows, 64-row
+// tiles (3 workgroups per CU) waste fewer padded rows and give split-K more
+// tiles to work with; above it, 128-row tiles (half the A re-reads and
+// dequantization per MFMA) with split-K when they underfill the chip.
+// Measured on the C3/C4 shapes: 64-row tiles without split-K lose to 128-row
+// tiles with split-K at M = 1152, N = 4096.
+static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& tiles_n, int& tiles,
+                       int& splits) {
   tiles_n = (w.N / 32 + 7) / 8;
-  tiles = tiles_n * ((M + 127) / 128);
+  mw = M <= 384 ? 64 : 128;
+  tiles = tiles_n * ((M + mw - 1) / mw);
   splits = choose_pipe_splits(tiles, w.K / 64, ncu);
 }
 
@@ -775,29 +774,29 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& tiles_n, int&
 size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   int s = choose_splits(M, w.N, w.K, MW, ncu);
-  int tiles_n, tiles, ps;
-  pipe_shape(w, M, ncu, tiles_n, tiles, ps);
+  int mw, tiles_n, tiles, ps;
+  pipe_shape(w, M, ncu, mw, tiles_n, tiles, ps);
   s = std::max(s, ps);
   return s > 1 ? (size_t)s * M * w.N * sizeof(float) : 0;
 }
 
-template <int FORM>
+template <int FORM, int MW>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
                              hipStream_t st) {
   const dim3 blk(256);
   switch (epi) {
-    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
   }
 }
 
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
                              float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
-  int tiles_n, tiles, splits;
-  pipe_shape(w, M, ncu, tiles_n, tiles, splits);
+  int mw, tiles_n, tiles, splits;
+  pipe_shape(w, M, ncu, mw, tiles_n, tiles, splits);
   GemmArgs g{};
   g.x = x;
   g.wp = w.wp;
@@ -816,11 +815,9 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
       return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
     g.part = workspace;
   }
-  static const int map = [] { const char* e = getenv("TGOHIP_GEMM_MAP"); return e ? atoi(e) : 0; }();
-  g.map = map;
-  const dim3 grid((unsigned)(map == 0 ? 8 * ((tiles_n + 7) / 8) * (tiles / tiles_n) : tiles), 1,
-                  (unsigned)splits);
-  launch_pipe_form<TGOHIP_FORM_I4_SYM>(g, epi, grid, tiles_n, tiles, st);
+  const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
+  if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_SYM, 128>(g, epi, grid, tiles_n, tiles, st);
+  else launch_pipe_form<TGOHIP_FORM_I4_SYM, 64>(g, epi, grid, tiles_n, tiles, st);
   if (splits > 1) launch_reduce(g, epi, splits, st);
   TGOHIP_HIP(hipGetLastError());
   return 0;
