@@ -971,6 +971,7 @@ struct tgohip_sched {
   uint64_t next = 0;
   // reusable host buffers
   std::vector<uint32_t> ids, posq, posk, slotv, lengths, extents, last, table;
+  int table_stride = 1;  // row stride of table: the longest lease of the last step
   std::vector<int32_t> argmax;
 };
 
@@ -1136,8 +1137,13 @@ int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, in
     maxp = std::max(maxp, (int)s->slots[i].pages.size());
     toks.insert(toks.end(), wtok[i].begin(), wtok[i].end());
   }
-  const int maxPages = s->ctx->kv_positions / m.block;
+  // The table's row stride is the longest lease of the step, not the whole
+  // pool (batch.go sizes it by the pool; only the stride differs, every row
+  // is still zero past its lease). At C4 this is ~600 entries instead of
+  // 25,000: the table shrinks from 13.6 MB to ~0.3 MB per step.
+  const int maxPages = maxp;
   std::vector<int32_t> pagesv((size_t)n * maxPages, 0), plens(n, 0);
+  s->table_stride = maxPages;
   s->table.assign((size_t)n * maxPages, 0u);
   for (int i = 0; i < n; i++) {
     plens[i] = (int32_t)s->slots[i].pages.size();
@@ -1264,7 +1270,7 @@ int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32
                            uint32_t* lengths, uint32_t* extents, uint32_t* last, uint32_t* pages) {
   *rows = (int32_t)s->ids.size();
   *batch = (int32_t)s->lengths.size();
-  *max_pages = s->ctx->kv_positions / s->ctx->cfg.block;
+  *max_pages = s->table_stride;
   auto cp = [](uint32_t* dst, const std::vector<uint32_t>& v) {
     if (dst) std::memcpy(dst, v.data(), v.size() * 4);
   };
