@@ -703,6 +703,31 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
     };
     std::stable_sort(dec.begin(), dec.end(), heavy);
+    // Beside prefill items (which keep every CU busy until late in the
+    // launch), decode groups (the kv heads of one part) are taken alternately
+    // from the long and the short end, so short items' start-up latency
+    // overlaps long items' streaming. Without prefill items, heavy-first keeps
+    // the tail short. TGOHIP_ATTN_ORDER = 0 / 1 forces one or the other.
+    static const int order = [] { const char* e = getenv("TGOHIP_ATTN_ORDER"); return e ? atoi(e) : -1; }();
+    if ((order == 1 || (order < 0 && !pre.empty())) && !dec.empty()) {
+      std::vector<std::pair<size_t, size_t>> grp;
+      for (size_t i = 0; i < dec.size();) {
+        size_t j = i + 1;
+        while (j < dec.size() && dec[j].seq == dec[i].seq && dec[j].kv_lo == dec[i].kv_lo) j++;
+        grp.push_back({i, j});
+        i = j;
+      }
+      std::vector<AttnItem> alt;
+      alt.reserve(dec.size());
+      size_t lo = 0, hi = grp.size();
+      bool front = true;
+      while (lo < hi) {
+        const auto g = front ? grp[lo++] : grp[--hi];
+        for (size_t k = g.first; k < g.second; k++) alt.push_back(dec[k]);
+        front = !front;
+      }
+      dec.swap(alt);
+    }
     std::vector<std::vector<AttnItem>> q(kXcd);
     for (const AttnItem& x : pre) q[(x.seq * 131 + x.kvh) % kXcd].push_back(x);
     for (auto& qq : q) std::stable_sort(qq.begin(), qq.end(), heavy);
