@@ -9,20 +9,28 @@
 //    its own (length, extent), so a mixed step computes bit-for-bit what the
 //    same sequences compute in separate steps.
 //  * A workgroup of 4 waves stages 64 positions of K and V (16 KiB each) in LDS
-//    per iteration with 16-byte coalesced loads through the page table, XOR-
-//    swizzled by position so MFMA operand reads are bank-conflict free. The next
-//    tile's loads are in flight while the current tile is computed.
-//  * Scores are S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with q split into an f16
-//    high and low part (two MFMAs), so the f32 query is carried to ~2^-22 and
-//    the product with the f16 key is accumulated in f32. The D layout of S^T is
-//    exactly the B-operand layout of O^T = V^T . P^T on v_mfma_f32_16x16x16_f16,
-//    so probabilities never leave registers; the online-softmax statistics of a
-//    row live in the same lanes as that row's output accumulators.
-//  * Items with at most 16 rows (decodes: 1 token x G query heads) let the four
-//    waves take different positions and merge in LDS. Items with more rows
-//    (prefill chunks) take 64 rows, 16 per wave, and share every staged tile.
-//    Contexts longer than kAttnSplit positions are split into parts whose
-//    partial (o, m, l) a second kernel merges in part order (deterministic).
+//    per iteration with 16-byte coalesced loads through the page table. K rows
+//    are 256-byte bank rows with 16-byte chunks XOR-swizzled by position; V is
+//    transposed on the way in, its 4-position groups XOR-swizzled by dim row.
+//    Barriers order LDS only, so the next tiles' loads stay in flight.
+//  * q is split into an f16 high and low part (two MFMAs), so the f32 query is
+//    carried to ~2^-22 and the product with the f16 key is accumulated in f32.
+//  * Decode-style items (<= 16 rows: 1 token x G query heads) run S^T = K.Q^T
+//    on v_mfma_f32_16x16x32_f16 and O^T = V^T.P^T on v_mfma_f32_16x16x16_f16
+//    (the D layout of the first is the B layout of the second). The four waves
+//    take different positions, merge in LDS, and keep kDecodeDepth tiles of
+//    loads in flight.
+//  * Prefill-style items take 128 rows (32 tokens x 4 heads), 32 per wave, on
+//    v_mfma_f32_32x32x16_f16 for both products; probabilities stay in
+//    registers (see attn_prefill).
+//  * Contexts longer than kAttnSplitDecode / kAttnSplitPrefill positions are
+//    split into parts whose partial (o, m, l) a second kernel merges in part
+//    order (deterministic). An in-kernel merge by the last part to arrive was
+//    measured slower: making a partial visible across XCDs takes a
+//    device-scope fence, which writes back the XCD's L2.
+//  * Launch order interleaves the two kinds of item (HBM-bound decode streams
+//    beside MFMA-bound prefill tiles) and routes each prefill stream to one
+//    XCD so its L2 serves the re-reads.
 #include "../common.h"
 
 #include <algorithm>
