@@ -88,8 +88,12 @@ int repack_enqueue(int form, const void* plane, const uint16_t* scales, const ui
                    int K, int N, PackedWeight& w, int nb_stride, int nb_off, hipStream_t st);
 int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t st);
 size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu);
+// With defer != nullptr a split-K launch leaves its partial planes in the
+// workspace ([splits][M][N] f32) and sets *defer = splits instead of running
+// the reduction; the caller folds them into the consumer (rmsnorm,
+// qk_rope_kv). *defer = 0 when the epilogue ran as usual.
 int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
-                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st);
+                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer = nullptr);
 
 // ---- attention (kernels/attention.hip) -----------------------------------
 struct AttnDevPlan {
@@ -111,7 +115,9 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
 
 // ---- per-row kernels (kernels/elementwise.hip) ---------------------------
 struct QKRopeArgs {
-  const float* qkv;       // [T, (H + 2*Hkv) * 128]
+  const float* qkv;       // [T, (H + 2*Hkv) * 128], or nsplit partial planes of it
+  int nsplit;             // 0: qkv is the projection; > 0: sum the planes (split order)
+  size_t plane;           // elements per partial plane
   const float* qnorm;     // [128]
   const float* knorm;     // [128]
   const uint32_t* posq;   // [T*H]
@@ -126,8 +132,9 @@ struct QKRopeArgs {
 };
 void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
                   int d, float* h, hipStream_t st);
-void launch_rmsnorm(const float* x, const uint32_t* rows, int nrows, const float* g, int w,
-                    float eps, void* out, int out_f16, hipStream_t st);
+void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
+                    float eps, void* out, int out_f16, hipStream_t st, const float* part = nullptr,
+                    int nsplit = 0, size_t plane = 0);
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st);
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
                    hipStream_t st);

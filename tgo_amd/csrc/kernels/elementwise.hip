@@ -49,15 +49,25 @@ __global__ void embed_kernel(const uint32_t* ids, const void* table, const uint1
 
 // out[r, :] = x[src(r), :] * rsqrt(mean(x^2) + eps) * g, stored f16 or f32.
 // src(r) = rows ? rows[r] : r. One 256-thread block per row.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint32_t* rows,
+// With nsplit > 0 the residual add of a split-K projection is still pending:
+// x[src, :] += sum_s part[s][src, :] (summed in split order, as
+// gemm_reduce_kernel would) is done here first and written back to x.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float* x, const uint32_t* rows,
                                                       const float* g, int w, float eps,
-                                                      void* out, int out_f16) {
+                                                      void* out, int out_f16, const float* part,
+                                                      int nsplit, size_t plane) {
   __shared__ float red[4];
   const int r = blockIdx.x;
   const size_t src = (size_t)(rows ? rows[r] : (uint32_t)r) * w;
   float ss = 0.f;
   for (int i = threadIdx.x * 4; i < w; i += 1024) {
-    const float4_t v = *(const float4_t*)(x + src + i);
+    float4_t v = *(const float4_t*)(x + src + i);
+    if (nsplit > 0) {
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < nsplit; sp++) acc += *(const float4_t*)(part + sp * plane + src + i);
+      v += acc;
+      *(float4_t*)(x + src + i) = v;
+    }
     ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
   }
   ss = block_sum256(ss, red);
@@ -84,13 +94,24 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int W = (a.H + 2 * a.Hkv) * kHeadDim;
   const float* row = a.qkv + (size_t)t * W;
+  // split-K projection: the row is the sum of the partial planes, in split order
+  auto load2 = [&](int off) -> float2 {
+    if (a.nsplit == 0) return *(const float2*)(row + off);
+    float2 acc = make_float2(0.f, 0.f);
+    for (int sp = 0; sp < a.nsplit; sp++) {
+      const float2 pv = *(const float2*)(a.qkv + sp * a.plane + (size_t)t * W + off);
+      acc.x += pv.x;
+      acc.y += pv.y;
+    }
+    return acc;
+  };
   const uint32_t slot = a.slots[t];
   const bool write = slot < (uint32_t)a.capacity;
   int cpos = -1;
   float c = 1.f, s = 0.f;
   const double inv = a.inv_freq[lane];
   for (int hh = wave; hh < a.H + 2 * a.Hkv; hh += 4) {
-    const float2 v = *(const float2*)(row + hh * kHeadDim + 2 * lane);
+    const float2 v = load2(hh * kHeadDim + 2 * lane);
     if (hh >= a.H + a.Hkv) {
       // value head: narrowed and scattered as is
       if (write) {
@@ -265,9 +286,11 @@ void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t*
                   int d, float* h, hipStream_t st) {
   hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, st, ids, table, scales, form, d, h);
 }
-void launch_rmsnorm(const float* x, const uint32_t* rows, int nrows, const float* g, int w,
-                    float eps, void* out, int out_f16, hipStream_t st) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, st, x, rows, g, w, eps, out, out_f16);
+void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
+                    float eps, void* out, int out_f16, hipStream_t st, const float* part,
+                    int nsplit, size_t plane) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, st, x, rows, g, w, eps, out, out_f16,
+                     part, nsplit, plane);
 }
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);

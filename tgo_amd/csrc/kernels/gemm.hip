@@ -794,7 +794,7 @@ static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n,
 }
 
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
-                             float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
+                             float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
   int mw, tiles_n, tiles, splits;
   pipe_shape(w, M, ncu, mw, tiles_n, tiles, splits);
   GemmArgs g{};
@@ -818,7 +818,8 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
   const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
   if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_SYM, 128>(g, epi, grid, tiles_n, tiles, st);
   else launch_pipe_form<TGOHIP_FORM_I4_SYM, 64>(g, epi, grid, tiles_n, tiles, st);
-  if (splits > 1) launch_reduce(g, epi, splits, st);
+  if (defer) *defer = splits > 1 ? splits : 0;
+  if (splits > 1 && !defer) launch_reduce(g, epi, splits, st);
   TGOHIP_HIP(hipGetLastError());
   return 0;
 }
@@ -840,9 +841,13 @@ static bool use_pipe(const PackedWeight& w, bool x_f32, int M) {
 }
 
 int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
-                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st) {
+                 float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
+  if (defer) *defer = 0;
   if (M <= 0) return 0;
-  if (use_pipe(w, x_f32, M)) return gemm_pipe_enqueue(w, x, M, y, epi, workspace, ws_bytes, ncu, st);
+  if (defer && epi != EPI_F32 && epi != EPI_RESID)
+    return fail(TGOHIP_ESTATE, "linear: only f32 and residual epilogues can defer split-K");
+  if (use_pipe(w, x_f32, M))
+    return gemm_pipe_enqueue(w, x, M, y, epi, workspace, ws_bytes, ncu, st, defer);
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   const int splits = choose_splits(M, w.N, w.K, MW, ncu);
   GemmArgs g{};
@@ -872,7 +877,8 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
     if (x_f32) launch_mw<128, true>(w.form, g, epi, grid, st);
     else launch_mw<128, false>(w.form, g, epi, grid, st);
   }
-  if (splits > 1) launch_reduce(g, epi, splits, st);
+  if (defer) *defer = splits > 1 ? splits : 0;
+  if (splits > 1 && !defer) launch_reduce(g, epi, splits, st);
   TGOHIP_HIP(hipGetLastError());
   return 0;
 }

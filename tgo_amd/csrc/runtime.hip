@@ -762,26 +762,41 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
     }
   }
   launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st);
+  // A split-K projection's partial planes are summed by the kernel that reads
+  // its output next (in split order, so the result is the reduction's):
+  // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
+  // rmsnorm. `pend` counts the planes of a residual add still owed to h.
+  const size_t plane = (size_t)T * m.hidden;
+  int pend = 0;
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
-    launch_rmsnorm(h, nullptr, T, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st);
-    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, T, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st))) return rc;
-    QKRopeArgs qa{(const float*)c->qkv.p, L.g_q, L.g_k, sg.dev<uint32_t>(c, o_posq),
-                  sg.dev<uint32_t>(c, o_posk), sg.dev<uint32_t>(c, o_slots), c->inv_freq,
-                  (float*)c->q.p, c->kc + l * layer_kv, c->vc + l * layer_kv, m.heads, m.kv_heads,
-                  c->kv_positions, m.rms_eps};
+    launch_rmsnorm(h, nullptr, T, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    int qkv_split = 0;
+    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, T, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
+                           &qkv_split)))
+      return rc;
+    QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
+                  (size_t)T * (m.heads + 2 * m.kv_heads) * kHeadDim, L.g_q, L.g_k,
+                  sg.dev<uint32_t>(c, o_posq), sg.dev<uint32_t>(c, o_posk),
+                  sg.dev<uint32_t>(c, o_slots), c->inv_freq, (float*)c->q.p, c->kc + l * layer_kv,
+                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps};
     launch_qk_rope_kv(qa, T, st);
     if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l], st));
     if ((rc = attn_enqueue(plan, dp, c->q.p, 0, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
     if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l + 1], st));
-    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st))) return rc;
-    launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st);
+    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
+      return rc;
+    launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
     if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, T, c->act.p,
                            f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
       return rc;
-    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st))) return rc;
+    // the last layer's residual add completes here (the head reads only Last rows)
+    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st,
+                           l + 1 < m.layers ? &pend : nullptr)))
+      return rc;
+    if (l + 1 == m.layers) pend = 0;
   }
   launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p, actf16, st);
   if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
