@@ -82,6 +82,18 @@ int tgohip_use_own_stream(tgohip_ctx* ctx);
  * high + low pair (two MFMAs), keeping ~22 bits of it -- tgo's f32-activation
  * semantics (nn/blocks.go:13-21) at twice the matrix-core work. */
 int tgohip_set_precision(tgohip_ctx* ctx, int mode);
+/* Prefix-shared (cascade) attention, the "read a shared page once" design of
+ * tgo's prefix cache (internal/prefix block sharing; specs/016-prefix-cache.md).
+ * No counterpart in the reference's kernels: tgo reads a shared page once per
+ * sequence. With min_sharers >= 2, decode rows of sequences whose page tables
+ * begin with the same pages (at least 64 positions, whole 64-position tiles
+ * visible to every row) attend to that shared prefix in one pass per group of
+ * up to 128/G sequences, and their own suffixes separately; the parts merge
+ * in a fixed order. 0 (the default) turns it off: every sequence is then
+ * decomposed as it would be alone, bit-for-bit (ragged_test.go:295), which a
+ * grouped prefix cannot promise (its results differ from the ungrouped ones
+ * within f32 rounding). */
+int tgohip_set_cascade(tgohip_ctx* ctx, int min_sharers);
 
 /* ---- model configuration: replaces model.Config (model/config.go) -------- */
 typedef struct {

@@ -259,3 +259,104 @@ def test_refusals_name_the_field(ctx, torch_gpu):
         run(ctx, torch_gpu, q, k, k, [20], [1], [0, 7], 2, 16, 0.5, 4, 2)
     with pytest.raises(tgo_amd.TgoError, match="extents sum"):
         run(ctx, torch_gpu, q, k, k, [5, 5], [1, 1], [0, 0, 1, 1], 2, 16, 0.5, 4, 2)
+
+
+def shared_prefix_inputs(seed, B, H, Hkv, block, prefix_pages, suffix_lo, suffix_hi, extra=0):
+    """B decode sequences whose page tables begin with the same prefix_pages
+    pages, each followed by its own pages (suffix lengths U[suffix_lo,
+    suffix_hi]), then `extra` unrelated decode sequences."""
+    rng = np.random.default_rng(seed)
+    P = prefix_pages * block
+    L = [P + int(rng.integers(suffix_lo, suffix_hi + 1)) for _ in range(B)]
+    L += [int(rng.integers(64, 700)) for _ in range(extra)]
+    B2 = B + extra
+    need = [(x + block - 1) // block for x in L]
+    own = [need[s] - (prefix_pages if s < B else 0) for s in range(B2)]
+    pool = prefix_pages + sum(own)
+    perm = rng.permutation(pool)
+    shared = perm[:prefix_pages]
+    at = prefix_pages
+    maxp = max(need)
+    pages = np.zeros((B2, maxp), np.uint32)
+    for s in range(B2):
+        row = list(shared) if s < B else []
+        row += list(perm[at:at + own[s]])
+        at += own[s]
+        pages[s, :len(row)] = row
+    k = rng.standard_normal((pool * block, Hkv, DH), dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((pool * block, Hkv, DH), dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal((B2, H, DH), dtype=np.float32)
+    return dict(L=np.array(L), ext=np.ones(B2, np.int64), pages=pages, maxp=maxp, k=k, v=v, q=q,
+                B=B2, H=H, Hkv=Hkv, block=block)
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (64, 8)])
+def test_shared_prefix_attention_matches_the_oracle(ctx, torch_gpu, H, Hkv):
+    """Prefix-shared (cascade) attention: 40 decode sequences over one 512-position
+    prefix plus their own suffixes, beside unrelated sequences. Every row equals
+    the ragged oracle to tgo's budget and the plain path within f32 rounding;
+    the result is the same on a second launch (deterministic)."""
+    c = shared_prefix_inputs(21, 40, H, Hkv, 16, 32, 1, 900, extra=5)
+    args = (c["q"], c["k"], c["v"], c["L"], c["ext"], c["pages"].ravel(), c["maxp"], c["block"],
+            1.0 / math.sqrt(DH), H, Hkv)
+    plain = run(ctx, torch_gpu, *args)
+    ctx.set_cascade(2)
+    try:
+        shared = run(ctx, torch_gpu, *args)
+        again = run(ctx, torch_gpu, *args)
+    finally:
+        ctx.set_cascade(0)
+    assert np.array_equal(shared, again)
+    assert not np.array_equal(shared, plain)  # the prefix really took the grouped path
+    for s in range(c["B"]):
+        want, b = oracle.ragged_attention_f64(c["q"][s:s + 1], H, Hkv, DH, c["k"], c["v"],
+                                              [c["L"][s]], [1], c["pages"][s], c["maxp"],
+                                              c["block"], 1.0 / math.sqrt(DH))
+        assert np.abs(shared[s:s + 1] - want).max() <= budget(b), s
+        assert np.abs(shared[s:s + 1] - plain[s:s + 1]).max() <= budget(b), s
+
+
+def test_shared_prefix_stops_where_the_tables_diverge(ctx, torch_gpu):
+    """Members sharing 8 pages with one that diverges after 5: the group's prefix
+    is cut to the whole tiles all of them share (4 pages = 64 positions)."""
+    c = shared_prefix_inputs(22, 6, 32, 8, 16, 8, 10, 200)
+    pages = c["pages"].copy()
+    pages[5, 5] = pages[5, 9]  # sequence 5 diverges at page 5
+    pages[5, 9] = c["pages"][5, 5]
+    args = (c["q"], c["k"], c["v"], c["L"], c["ext"], pages.ravel(), c["maxp"], c["block"],
+            1.0 / math.sqrt(DH), 32, 8)
+    ctx.set_cascade(2)
+    try:
+        got = run(ctx, torch_gpu, *args)
+    finally:
+        ctx.set_cascade(0)
+    for s in range(c["B"]):
+        want, b = oracle.ragged_attention_f64(c["q"][s:s + 1], 32, 8, DH, c["k"], c["v"],
+                                              [c["L"][s]], [1], pages[s], c["maxp"], c["block"],
+                                              1.0 / math.sqrt(DH))
+        assert np.abs(got[s:s + 1] - want).max() <= budget(b), s
+
+
+def test_c5_shaped_shared_prefix_sampled_rows(ctx, torch_gpu):
+    """BASELINE config 5's attention shape: 256 sequences over one 2048-token prefix
+    (128 pages of 16) plus unique suffixes U[32, 1024], 64 q / 8 kv heads. Sampled
+    rows against the oracle; all rows against the plain path."""
+    c = shared_prefix_inputs(5, 256, 64, 8, 16, 128, 32, 1024)
+    args = (c["q"], c["k"], c["v"], c["L"], c["ext"], c["pages"].ravel(), c["maxp"], c["block"],
+            1.0 / math.sqrt(DH), 64, 8)
+    plain = run(ctx, torch_gpu, *args)
+    ctx.set_cascade(2)
+    try:
+        shared = run(ctx, torch_gpu, *args)
+    finally:
+        ctx.set_cascade(0)
+    rng = np.random.default_rng(3)
+    for s in rng.choice(256, 6, replace=False):
+        want, b = oracle.ragged_attention_f64(c["q"][s:s + 1], 64, 8, DH, c["k"], c["v"],
+                                              [c["L"][s]], [1], c["pages"][s], c["maxp"],
+                                              c["block"], 1.0 / math.sqrt(DH))
+        assert np.abs(shared[s:s + 1] - want).max() <= budget(b), s
+    # both paths round probabilities to f16 for the PV MFMA, against different
+    # running maxima: each is within 2^-11 of exact, so they agree to 2^-10
+    rel = np.abs(shared - plain).max() / np.abs(plain).max()
+    assert rel <= 2.0 ** -10, rel

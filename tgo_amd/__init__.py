@@ -67,6 +67,7 @@ def lib():
         "tgohip_sync": (I, [P]),
         "tgohip_set_stream": (I, [P, P]),
         "tgohip_set_precision": (I, [P, I]),
+        "tgohip_set_cascade": (I, [P, I]),
         "tgohip_use_own_stream": (I, [P]),
         "tgohip_config": (I, [P, ctypes.POINTER(ModelCfg)]),
         "tgohip_weight": (I, [P, ctypes.c_char_p, I, I, I, P, P, P]),
@@ -344,6 +345,11 @@ class Context:
 
     def sync(self):
         check(lib().tgohip_sync(self.h))
+
+    def set_cascade(self, min_sharers):
+        """Prefix-shared attention for groups of at least min_sharers decode
+        sequences whose page tables begin alike (0: off, the default)."""
+        check(lib().tgohip_set_cascade(self.h, min_sharers))
 
     def set_precision(self, mode):
         check(lib().tgohip_set_precision(self.h, mode))

@@ -41,9 +41,13 @@ struct AttnItem {
   int32_t kv_hi;
   int32_t part;  // partial slot for a split item, -1 when the item writes `out`
   int32_t mode;  // 0: rows <= 16, the four waves split the positions; 1: waves split rows;
-                 // 2: an empty slot of the launch order
+                 // 2: an empty slot of the launch order; 3: a shared prefix: rows are
+                 // the decode tokens of sequences seqlist[tok0 .. tok0+ntok) (G rows
+                 // each), pages those of `seq`, every position visible
 };
-// One combine item: merges nparts partial results of a (sequence, kv head, tokens).
+// One combine item: merges the partial results of a (sequence, kv head,
+// tokens): first xparts parts of a shared prefix (the sequence's rows sit at
+// row xrow of those parts), then nparts parts of its own positions.
 struct AttnCombine {
   int32_t seq;
   int32_t kvh;
@@ -51,18 +55,24 @@ struct AttnCombine {
   int32_t ntok;
   int32_t part0;
   int32_t nparts;
-  int32_t pad0, pad1;
+  int32_t xpart0;  // first shared-prefix part, -1 when none
+  int32_t xparts;
+  int32_t xrow;
+  int32_t pad;
 };
 
 constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
 constexpr int kAttnSplitDecode = 4096;   // positions per part of a split decode-style item
 constexpr int kAttnSplitPrefill = 2048;  // positions per part of a split prefill-style item
+constexpr int kAttnSplitShared = 512;    // positions per part of a shared-prefix item
 constexpr int kAttnRowsP = 128;   // rows per prefill-style item (4 waves x 32)
 constexpr int kHeadDim = 128;
 
 struct AttnPlan {
   std::vector<AttnItem> items;
   std::vector<AttnCombine> combines;
+  std::vector<int32_t> seqlist;  // sequences of shared-prefix items
+  int64_t shared_positions = 0;  // positions read once for a group instead of per sequence
   std::vector<int32_t> cu;  // [B] flat row offset of each sequence
   int parts = 0;
   int claimed = 0;          // sum of extents
@@ -99,6 +109,7 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
 struct AttnDevPlan {
   const AttnItem* items;
   const AttnCombine* combines;
+  const int32_t* seqlist;
   const int32_t* cu;
   const uint32_t* lengths;
   const uint32_t* extents;
@@ -108,7 +119,7 @@ struct AttnDevPlan {
 };
 int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
                     const uint32_t* pages, int max_pages, int block, int capacity, int H,
-                    int Hkv, AttnPlan& plan);
+                    int Hkv, AttnPlan& plan, int cascade_min = 0);
 int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int q_f16,
                  const void* k, const void* v, void* out, int out_f16, int T, int H, int Hkv,
                  int max_pages, int block, float scale, hipStream_t stream);

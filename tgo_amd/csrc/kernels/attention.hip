@@ -48,6 +48,7 @@ struct AttnArgs {
   float* part_ml;  // [parts][128]: m[64] then l[64]
   const AttnItem* items;
   const AttnCombine* combines;
+  const int32_t* seqlist;
   const int32_t* cu;
   const uint32_t* lengths;
   const uint32_t* extents;
@@ -375,18 +376,23 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
   const int G = c.G, R = it.ntok * G;
   const int r = wave * 32 + l32;
   const bool valid = r < R;
-  const int tok = it.tok0 + (valid ? r / G : 0);
+  // A shared-prefix item's rows are the decode tokens of several sequences,
+  // each of which sees every prefix position.
+  const bool shared = it.mode == 3;
+  const int rseq = shared ? a.seqlist[it.tok0 + (valid ? r / G : 0)] : c.s;
+  const int tok = shared ? 0 : it.tok0 + (valid ? r / G : 0);
   const int head = c.kvh * G + (valid ? r % G : 0);
-  const int lim = valid ? (c.L - c.n + tok) : -1;
+  const int lim = !valid ? -1 : shared ? it.kv_hi : (c.L - c.n + tok);
   // Positions every valid row of this wave may see (its first token's limit),
   // and whether the wave's rows are all valid.
   const int wtok0 = it.tok0 + (wave * 32) / G;
-  const int wave_hi = min(it.kv_hi, c.L - c.n + wtok0 + 1);
+  const int wave_hi = shared ? it.kv_hi : min(it.kv_hi, c.L - c.n + wtok0 + 1);
   const bool wave_full = wave * 32 + 32 <= R;
+  const int rcu = shared ? a.cu[rseq] : c.cu;
 
   half8_t qh[8], ql[8];
   {
-    const size_t qoff = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
+    const size_t qoff = ((size_t)(rcu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
     for (int ss = 0; ss < 8; ss++) attn_load_q(a, qoff + 16 * ss + 8 * kh, valid, qh[ss], ql[ss]);
   }
@@ -480,7 +486,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
   // Lane (r, kh) holds dims 32db + 8g + 4kh + [0,4) of row r, g = 0..3.
   if (it.part < 0) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    const size_t base = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
+    const size_t base = ((size_t)(rcu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; db++)
 #pragma unroll
@@ -558,16 +564,23 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   {
     const int row = (int)blockIdx.y * 16 + (tid >> 4);  // 16 rows per block
     if (row >= R) return;
+    // parts in merge order: the shared prefix's (at row xrow + row), then the
+    // sequence's own (at row)
+    const int np = cb.xparts + cb.nparts;
     float mstar = -INFINITY;
-    for (int p = 0; p < cb.nparts; p++)
-      mstar = fmaxf(mstar, a.part_ml[(size_t)(cb.part0 + p) * 2 * kAttnRowsP + row]);
+    for (int p = 0; p < np; p++) {
+      const size_t part = (size_t)(p < cb.xparts ? cb.xpart0 + p : cb.part0 + p - cb.xparts);
+      const int pr = p < cb.xparts ? cb.xrow + row : row;
+      mstar = fmaxf(mstar, a.part_ml[part * 2 * kAttnRowsP + pr]);
+    }
     float lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int p = 0; p < cb.nparts; p++) {
-      const size_t part = (size_t)(cb.part0 + p);
-      const float mw = a.part_ml[part * 2 * kAttnRowsP + row];
+    for (int p = 0; p < np; p++) {
+      const size_t part = (size_t)(p < cb.xparts ? cb.xpart0 + p : cb.part0 + p - cb.xparts);
+      const int pr = p < cb.xparts ? cb.xrow + row : row;
+      const float mw = a.part_ml[part * 2 * kAttnRowsP + pr];
       const float wt = (mw == -INFINITY) ? 0.f : exp2f(mw - mstar);
-      lsum += wt * a.part_ml[part * 2 * kAttnRowsP + kAttnRowsP + row];
-      const float* src = a.part_o + (part * kAttnRowsP + row) * 128 + d0;
+      lsum += wt * a.part_ml[part * 2 * kAttnRowsP + kAttnRowsP + pr];
+      const float* src = a.part_o + (part * kAttnRowsP + pr) * 128 + d0;
 #pragma unroll
       for (int j = 0; j < 8; j++) acc[j] += wt * src[j];
     }
@@ -595,7 +608,7 @@ __global__ void zero_rows_kernel(void* out, int f16, size_t start, size_t count)
 // position a claimed row reads has a page-table entry inside the pool.
 int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
                     const uint32_t* pages, int max_pages, int block, int capacity, int H,
-                    int Hkv, AttnPlan& plan) {
+                    int Hkv, AttnPlan& plan, int cascade_min) {
   if (H <= 0 || Hkv <= 0 || H % Hkv != 0)
     return fail(TGOHIP_EINVAL, "attention: query heads " + std::to_string(H) +
                                    " are not a multiple of kv heads " + std::to_string(Hkv));
@@ -606,6 +619,8 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
   if (block <= 0) return fail(TGOHIP_EINVAL, "attention: block is " + std::to_string(block));
   plan.items.clear();
   plan.combines.clear();
+  plan.seqlist.clear();
+  plan.shared_positions = 0;
   plan.cu.assign(B, 0);
   plan.parts = 0;
   int64_t at = 0;
@@ -652,9 +667,90 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
     const int v = e ? atoi(e) : kAttnSplitPrefill;
     return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplitPrefill;
   }();
+  // Shared prefixes (opt-in): decode sequences (one token) whose page rows
+  // begin with the same pages attend to those positions together. A group's
+  // prefix is the longest run of pages every member shares, cut to whole
+  // 64-position tiles and to positions every member's token sees. Each batch
+  // of up to 128/G members gets items over the prefix (split like prefill
+  // items) writing partials; each member's own suffix is decode items writing
+  // partials; the combine merges prefix parts, then suffix parts.
+  std::vector<int> cpos(B, 0), cbase(B, 0), cnsp(B, 0), crow(B, 0);
+  if (cascade_min >= 2) {
+    std::vector<std::pair<uint32_t, int>> firsts;
+    for (int s = 0; s < B; s++)
+      if (extents[s] == 1 && G <= 16 && (int)lengths[s] >= kAttnTile)
+        firsts.push_back({pages[(size_t)s * max_pages], s});
+    std::stable_sort(firsts.begin(), firsts.end(),
+                     [](const std::pair<uint32_t, int>& x, const std::pair<uint32_t, int>& y) {
+                       return x.first < y.first;
+                     });
+    for (size_t i = 0; i < firsts.size();) {
+      size_t j = i + 1;
+      while (j < firsts.size() && firsts[j].first == firsts[i].first) j++;
+      if ((int)(j - i) >= cascade_min) {
+        const int lead = firsts[i].second;
+        const uint32_t* lrow = pages + (size_t)lead * max_pages;
+        int64_t ppos = lengths[lead];
+        for (size_t k = i; k < j; k++) {
+          const int sq = firsts[k].second;
+          const uint32_t* row = pages + (size_t)sq * max_pages;
+          const int64_t need = std::min<int64_t>((lengths[sq] + block - 1) / block,
+                                                 (lengths[lead] + block - 1) / block);
+          int64_t cp = 0;
+          while (cp < need && row[cp] == lrow[cp]) cp++;
+          ppos = std::min<int64_t>(ppos, std::min<int64_t>(cp * block, lengths[sq]));
+        }
+        ppos = ppos / kAttnTile * kAttnTile;
+        if (ppos >= kAttnTile) {
+          // Prefix parts are short: a group's few prefix items would otherwise
+          // be the launch's longest chains.
+          const int xsplit = std::min(psplit, kAttnSplitShared);
+          const int per = std::max(1, kAttnRowsP / G);
+          const int nsp = (int)((ppos + xsplit - 1) / xsplit);
+          for (size_t b0 = i; b0 < j; b0 += per) {
+            const int nb = (int)std::min<size_t>(per, j - b0);
+            const int base = plan.parts;
+            plan.parts += Hkv * nsp;
+            const int off = (int)plan.seqlist.size();
+            for (int k = 0; k < nb; k++) {
+              const int sq = firsts[b0 + k].second;
+              plan.seqlist.push_back(sq);
+              cpos[sq] = (int)ppos;
+              cbase[sq] = base;
+              cnsp[sq] = nsp;
+              crow[sq] = k * G;
+            }
+            for (int kvh = 0; kvh < Hkv; kvh++)
+              for (int p = 0; p < nsp; p++)
+                plan.items.push_back(AttnItem{lead, kvh, off, nb, p * xsplit,
+                                              (int)std::min<int64_t>(ppos, (int64_t)(p + 1) * xsplit),
+                                              base + kvh * nsp + p, 3});
+          }
+          plan.shared_positions += (int64_t)(j - i - 1) * ppos;
+        }
+      }
+      i = j;
+    }
+  }
   for (int s = 0; s < B; s++) {
     const int n = (int)extents[s], L = (int)lengths[s];
     if (n == 0) continue;
+    if (cpos[s] > 0) {
+      // the suffix after the shared prefix, always as partials
+      const int lo0 = cpos[s];
+      const int splits = (L - lo0 + split - 1) / split;
+      const int base = plan.parts;
+      for (int p = 0; p < splits; p++) {
+        const int lo = lo0 + p * split, hi = std::min(L, lo + split);
+        for (int kvh = 0; kvh < Hkv; kvh++)
+          plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, 0});
+      }
+      for (int kvh = 0; kvh < Hkv; kvh++)
+        plan.combines.push_back(AttnCombine{s, kvh, 0, n, base + kvh * splits, splits,
+                                            cbase[s] + kvh * cnsp[s], cnsp[s], crow[s], 0});
+      plan.parts += Hkv * splits;
+      continue;
+    }
     if (n * G <= 16) {
       // The kv heads of one part are adjacent in launch order: they read the
       // same 2 KiB position rows of the pool at about the same time.
@@ -669,7 +765,7 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
             plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, 0});
         }
         for (int kvh = 0; kvh < Hkv; kvh++)
-          plan.combines.push_back(AttnCombine{s, kvh, 0, n, base + kvh * splits, splits, 0, 0});
+          plan.combines.push_back(AttnCombine{s, kvh, 0, n, base + kvh * splits, splits, -1, 0, 0, 0});
         plan.parts += Hkv * splits;
       }
     } else {
@@ -689,7 +785,7 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
               const int lo = p * psplit, h2 = std::min(hi, lo + psplit);
               plan.items.push_back(AttnItem{s, kvh, t0, nt, lo, h2, plan.parts++, 1});
             }
-            plan.combines.push_back(AttnCombine{s, kvh, t0, nt, part0, splits, 0, 0});
+            plan.combines.push_back(AttnCombine{s, kvh, t0, nt, part0, splits, -1, 0, 0, 0});
           }
         }
       }
@@ -777,6 +873,7 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
   a.part_ml = dp.part_ml;
   a.items = dp.items;
   a.combines = dp.combines;
+  a.seqlist = dp.seqlist;
   a.cu = dp.cu;
   a.lengths = dp.lengths;
   a.extents = dp.extents;

@@ -82,6 +82,7 @@ struct tgohip_ctx {
   half_t* vc = nullptr;
   int kv_positions = 0;
   int precision = 0;  // 0: f16 activations into MFMA, 1: f32 activations (hi+lo)
+  int cascade = 0;    // minimum sequences sharing a prefix for prefix-shared attention (0: off)
   // activations and workspaces
   DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, meta, gemm_ws, part_o, part_ml;
   int rows_cap = 0, batch_cap = 0;
@@ -483,6 +484,14 @@ int tgohip_sync(tgohip_ctx* c) {
   return 0;
 }
 
+int tgohip_set_cascade(tgohip_ctx* c, int min_sharers) {
+  if (min_sharers != 0 && min_sharers < 2)
+    return fail(TGOHIP_EINVAL, "cascade: min_sharers is 0 (off) or at least 2, not " +
+                                   std::to_string(min_sharers));
+  c->cascade = min_sharers;
+  return 0;
+}
+
 int tgohip_set_precision(tgohip_ctx* c, int mode) {
   if (mode != 0 && mode != 1) return fail(TGOHIP_EINVAL, "precision is 0 (f16 activations) or 1 (f32 activations)");
   c->precision = mode;
@@ -713,7 +722,7 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   }
   AttnPlan plan;
   int rc = attn_build_plan(T, B, s->lengths, s->extents, s->pages, s->max_pages, m.block,
-                           c->kv_positions, m.heads, m.kv_heads, plan);
+                           c->kv_positions, m.heads, m.kv_heads, plan, c->cascade);
   if (rc) return rc;
   if ((rc = ensure_activations(c, T, B))) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
@@ -731,13 +740,15 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
   const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
   const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  const size_t o_seql = sg.add(plan.seqlist.data(), plan.seqlist.size() * sizeof(int32_t));
   if ((rc = sg.upload(c))) return rc;
   const hipStream_t st = c->stream;
   TGOHIP_HIP(hipEventRecord(c->ev0, st));
 
   const uint32_t* d_ids = sg.dev<uint32_t>(c, o_ids);
   const uint32_t* d_ext = sg.dev<uint32_t>(c, o_ext);
-  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb),
+                 sg.dev<int32_t>(c, o_seql), sg.dev<int32_t>(c, o_cu),
                  sg.dev<uint32_t>(c, o_len), d_ext, sg.dev<uint32_t>(c, o_pages),
                  (float*)c->part_o.p, (float*)c->part_ml.p};
   const bool f32act = c->precision == 1;
@@ -755,6 +766,7 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
     for (int b = 0; b < B; b++)
       if (s->extents[b] > 0) attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
     attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (4 + (f32act ? 4 : 2));
+    attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
     while ((int)c->prof_ev.size() < 2 * m.layers) {
       hipEvent_t e;
       TGOHIP_HIP(hipEventCreate(&e));
@@ -843,7 +855,8 @@ int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int
   if ((int64_t)capacity * H_kv * kHeadDim >= (int64_t)1 << 31)
     return fail(TGOHIP_EINVAL, "attention: the cache view exceeds 32-bit element offsets");
   AttnPlan plan;
-  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan);
+  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan,
+                           c->cascade);
   if (rc) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
   Stager sg;
@@ -853,8 +866,10 @@ int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int
   const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
   const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
   const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  const size_t o_seql = sg.add(plan.seqlist.data(), plan.seqlist.size() * sizeof(int32_t));
   if ((rc = sg.upload(c))) return rc;
-  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb),
+                 sg.dev<int32_t>(c, o_seql), sg.dev<int32_t>(c, o_cu),
                  sg.dev<uint32_t>(c, o_len), sg.dev<uint32_t>(c, o_ext), sg.dev<uint32_t>(c, o_pages),
                  (float*)c->part_o.p, (float*)c->part_ml.p};
   return attn_enqueue(plan, dp, q, q_dtype == TGOHIP_F16, k, v, out, out_dtype == TGOHIP_F16, T, H,
@@ -869,7 +884,8 @@ int tgohip_paged_attention_replay(tgohip_ctx* c, const void* q, int q_dtype, int
                                   const uint32_t* pages, int max_pages, int block, float scale,
                                   void* out, int out_dtype, int iters) {
   AttnPlan plan;
-  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan);
+  int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan,
+                           c->cascade);
   if (rc) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
   Stager sg;
@@ -879,8 +895,10 @@ int tgohip_paged_attention_replay(tgohip_ctx* c, const void* q, int q_dtype, int
   const size_t o_cu = sg.add(plan.cu.data(), (size_t)B * 4);
   const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
   const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
+  const size_t o_seql = sg.add(plan.seqlist.data(), plan.seqlist.size() * sizeof(int32_t));
   if ((rc = sg.upload(c))) return rc;
-  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb), sg.dev<int32_t>(c, o_cu),
+  AttnDevPlan dp{sg.dev<AttnItem>(c, o_items), sg.dev<AttnCombine>(c, o_comb),
+                 sg.dev<int32_t>(c, o_seql), sg.dev<int32_t>(c, o_cu),
                  sg.dev<uint32_t>(c, o_len), sg.dev<uint32_t>(c, o_ext), sg.dev<uint32_t>(c, o_pages),
                  (float*)c->part_o.p, (float*)c->part_ml.p};
   for (int i = 0; i < iters; i++)
