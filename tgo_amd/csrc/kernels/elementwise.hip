@@ -145,35 +145,64 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
 }
 
 // First index of the strict maximum of each row (sample/stages.go:196-206).
-__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int V,
-                                                     const uint32_t* extents, int32_t* out) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  const int b = blockIdx.x;
+// Go's loop keeps best = x[0] and takes i only when x[i] > best: the first
+// index of the maximum, NaN never taken after index 0, and 0 when x[0] is NaN
+// or nothing exceeds it. One 1024-thread block per row; each thread scans its
+// 16-byte chunks in increasing index order, then the block reduces (larger
+// value, or equal value at a smaller index).
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V,
+                                                      const uint32_t* extents, int32_t* out) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float* row = logits + (size_t)b * V;
   float best = -INFINITY;
-  int bi = -1;
-  for (int i = threadIdx.x; i < V; i += 256) {
-    const float v = row[i];
-    if (bi < 0 || v > best) { best = v; bi = i; }
-  }
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o) {
-      const float v2 = sv[threadIdx.x + o];
-      const int i2 = si[threadIdx.x + o];
-      const float v1 = sv[threadIdx.x];
-      const int i1 = si[threadIdx.x];
-      if (i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1))) {
-        sv[threadIdx.x] = v2;
-        si[threadIdx.x] = i2;
-      }
+  int bi = 0x7fffffff;
+  const int V4 = V / 4;
+  const float4_t* row4 = (const float4_t*)row;  // rows are 16-byte aligned when V % 4 == 0
+  if ((V & 3) == 0) {
+    for (int i4 = t; i4 < V4; i4 += 1024) {
+      const float4_t v = row4[i4];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (v[j] > best) {
+          best = v[j];
+          bi = 4 * i4 + j;
+        }
     }
-    __syncthreads();
+  } else {
+    for (int i = t; i < V; i += 1024)
+      if (row[i] > best) {
+        best = row[i];
+        bi = i;
+      }
   }
-  if (threadIdx.x == 0) out[b] = extents[b] == 0 ? -1 : si[0];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(best, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    if (v2 > best || (v2 == best && i2 < bi)) {
+      best = v2;
+      bi = i2;
+    }
+  }
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < 16; w++)
+      if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+        best = sv[w];
+        bi = si[w];
+      }
+    // x[0] itself, and NaN at x[0], are Go's starting point
+    const float x0 = row[0];
+    int r = bi;
+    if (x0 != x0 || bi == 0x7fffffff || !(best > x0)) r = 0;
+    out[b] = extents[b] == 0 ? -1 : r;
+  }
 }
 
 // Zeroes the logits rows of members that contributed nothing.
@@ -297,7 +326,7 @@ void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
 }
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
                    hipStream_t st) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, st, logits, V, extents, out);
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out);
 }
 void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st) {
   hipLaunchKernelGGL(zero_idle_rows_kernel, dim3(B), dim3(256), 0, st, logits, V, extents);
