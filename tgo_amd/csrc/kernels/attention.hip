@@ -82,16 +82,31 @@ __device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const
   }
 }
 
-constexpr int kVtStride = kAttnTile + 8;  // halves per transposed-V row (bank spread)
 constexpr int kMaxItemPages = 1024;        // page indices an item stages in LDS
-constexpr int kAttnSmem = 16384 + 128 * kVtStride * 2 + kMaxItemPages * 4;
+constexpr int kAttnVBytes = 20480;         // one V tile in LDS (64 padded rows)
+constexpr int kAttnSmem = 16384 + kAttnVBytes + kMaxItemPages * 4;
 
-// Offset (halves) of transposed-V element (dim row, position c), c a multiple
-// of 4. Groups of 4 positions are XOR-swizzled by 9*(row/16) so the
-// transposing stores (16 lanes on rows 8 apart) and the MFMA operand reads (16
-// or 32 consecutive rows) all spread over the 64 banks.
-__device__ __forceinline__ int vt_off(int row, int c) {
-  return row * kVtStride + ((((c >> 2) ^ (((row >> 4) * 9) & 15))) << 2);
+// V tiles live in LDS row-major, 256 bytes per position at a row pitch of
+// 320 bytes, nudged by 32 bytes when bit 2 of the position is set and by 16
+// when bit 3 is: the 16-byte bank slot of (position p, chunk c) is then
+// (4(p&3) + 2((p>>2)&1) + ((p>>3)&1) + c) mod 16, so the 16-lane stores of one
+// position and the transposing operand reads below (8 positions x 2 chunks,
+// or 4 positions x 4 chunks per 32 lanes) touch distinct slots. The offset is
+// additive in multiples of 16 positions and in the dim, so each lane needs one
+// address register. Offset in halves of (position p, dim d):
+__device__ __forceinline__ int v_off(int p, int d) {
+  return 160 * p + 16 * ((p >> 2) & 1) + 8 * ((p >> 3) & 1) + d;
+}
+
+// The A operand of O^T = V^T.P^T, four positions of one dim per lane, read
+// straight from row-major V with gfx950's transposing LDS read: in each
+// 16-lane group, lane j names the 8 bytes at V[p0 + j/4][d0 + 4(j%4)], and
+// lane i receives V[p0 + k][d0 + i] for k = 0..3.
+__device__ __forceinline__ half4_t attn_vt4(const half_t* Vs, int p0, int d0, int j) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(Vs + v_off(p0 + (j >> 2), d0 + 4 * (j & 3))));
+  return __builtin_bit_cast(half4_t, r);
 }
 
 // A workgroup barrier that orders LDS only: global loads in flight stay in
@@ -151,22 +166,17 @@ __device__ __forceinline__ void attn_load_tile(const AttnArgs& a, const AttnCtx&
   }
 }
 
-// Writes a loaded tile to LDS: K row-major (one 256-byte bank row per
-// position, 16-byte chunks XOR-swizzled by position), V transposed.
-__device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, half_t* Vt,
+// Writes a loaded tile to LDS: K row-major, one 256-byte bank row per
+// position, 16-byte chunks XOR-swizzled by position; V row-major in padded
+// rows (v_off).
+__device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, half_t* Vs,
                                                 const uint4 (&kr)[4], const uint4 (&vr)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pos = c.pgrp + 16 * i;
     ((uint4*)Ks)[pos * 16 + (c.dch ^ (pos & 15))] = kr[i];
-  }
-  union U { uint4 u; half8_t h; };
-  U v0, v1, v2, v3;
-  v0.u = vr[0]; v1.u = vr[1]; v2.u = vr[2]; v3.u = vr[3];
-#pragma unroll
-  for (int d = 0; d < 8; d++) {
-    const half4_t col = {v0.h[d], v1.h[d], v2.h[d], v3.h[d]};
-    *(half4_t*)(Vt + vt_off(c.dch * 8 + d, 4 * c.pgrp)) = col;
+    const int pv = 4 * c.pgrp + i;
+    *(uint4*)(Vs + v_off(pv, 8 * c.dch)) = vr[i];
   }
 }
 
@@ -213,7 +223,7 @@ template <int BLK>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                             char* smem) {
   half_t* Ks = (half_t*)smem;
-  half_t* Vt = (half_t*)(smem + 16384);
+  half_t* Vs = (half_t*)(smem + 16384);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int G = c.G, R = it.ntok * G;
@@ -250,7 +260,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
       const int t0 = tt + u * kAttnTile;
       if (t0 < it.kv_hi) {
         attn_lds_barrier();  // the previous tile's LDS reads are done
-        attn_store_tile(c, Ks, Vt, kr[u], vr[u]);
+        attn_store_tile(c, Ks, Vs, kr[u], vr[u]);
         attn_lds_barrier();
         if (t0 + D * kAttnTile < it.kv_hi)
           attn_load_tile<BLK>(a, c, t0 + D * kAttnTile, it.kv_hi, kr[u], vr[u]);
@@ -301,7 +311,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           // O^T += V^T . P^T; the A operand is V^T[dim 16db+li][pos 16mb+4lg..+3].
 #pragma unroll
           for (int db = 0; db < 8; db++) {
-            const half4_t va = *(const half4_t*)(Vt + vt_off(db * 16 + li, mb * 16 + 4 * lg));
+            const half4_t va = attn_vt4(Vs, mb * 16 + 4 * lg, db * 16, li);
             o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[db], 0, 0, 0);
           }
         }
@@ -370,7 +380,7 @@ template <int BLK>
 __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                              char* smem) {
   half_t* Ks = (half_t*)smem;
-  half_t* Vt = (half_t*)(smem + 16384);
+  half_t* Vs = (half_t*)(smem + 16384);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
   const int G = c.G, R = it.ntok * G;
@@ -408,7 +418,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
   if (it.kv_lo < it.kv_hi) attn_load_tile<BLK>(a, c, it.kv_lo, it.kv_hi, kr, vr);
   for (int t0 = it.kv_lo; t0 < it.kv_hi; t0 += kAttnTile) {
     attn_lds_barrier();
-    attn_store_tile(c, Ks, Vt, kr, vr);
+    attn_store_tile(c, Ks, Vs, kr, vr);
     attn_lds_barrier();
     if (t0 + kAttnTile < it.kv_hi) attn_load_tile<BLK>(a, c, t0 + kAttnTile, it.kv_hi, kr, vr);
     float16_t sc[2];
@@ -461,22 +471,20 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
     m = mnew;
 #pragma unroll
     for (int db = 0; db < 4; db++) o[db] *= alpha;
-    // vt_off(32db + l32, 32pb + 16t + 8e + 4kh) written out: the position
-    // group 8pb + 4t + 2e + kh is XORed with 9*(2db + l32/16) mod 16, i.e. with
-    // 2db (bits 1-2) and the lane's 9*(l32/16) (bits 0, 3), so one lane value
-    // serves every read.
-    const int vrow = l32 * kVtStride, vcol = (kh ^ (9 * (l32 >> 4))) << 2;
+    // The PV operand of lane (l32, kh): dim 32db + l32, positions
+    // 32pb + 16t + 4kh + [0,4) and the same + 8 -- two transposing reads whose
+    // 16-lane groups take dims 32db + 16*(l32/16) + [0,16).
+    const int j16 = lane & 15, dgrp = 16 * ((lane >> 4) & 1);
 #pragma unroll
     for (int pb = 0; pb < 2; pb++)
 #pragma unroll
       for (int t = 0; t < 2; t++) {
+        const int p0 = pb * 32 + 16 * t + 4 * kh;
 #pragma unroll
         for (int db = 0; db < 4; db++) {
-          const int k0 = ((8 * pb + 4 * t) ^ (2 * db)) << 2, k1 = ((8 * pb + 4 * t + 2) ^ (2 * db)) << 2;
-          const half_t* vb = Vt + db * 32 * kVtStride;
-          const half4_t v0 = *(const half4_t*)(vb + vrow + (vcol ^ k0));
-          const half4_t v1 = *(const half4_t*)(vb + vrow + (vcol ^ k1));
-          const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          const half4_t v0 = attn_vt4(Vs, p0, db * 32 + dgrp, j16);
+          const half4_t v1 = attn_vt4(Vs, p0 + 8, db * 32 + dgrp, j16);
+          const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[pb][t], o[db], 0, 0, 0);
         }
       }
@@ -540,7 +548,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // Element offsets of one layer's pool fit 32 bits (the host checks).
   c.rstride = (uint32_t)a.Hkv * kHeadDim;
   c.prow = a.pages + (size_t)c.s * a.max_pages;
-  uint32_t* pg = (uint32_t*)(smem + 16384 + 128 * kVtStride * 2);
+  uint32_t* pg = (uint32_t*)(smem + 16384 + kAttnVBytes);
   c.pg = pg;
   c.pg0 = it.kv_lo / c.blk;
   const int npg = it.kv_hi > it.kv_lo ? (it.kv_hi - 1) / c.blk - c.pg0 + 1 : 0;
