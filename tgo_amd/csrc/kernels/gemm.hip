@@ -51,15 +51,23 @@ __device__ __forceinline__ half2_t as_h2(uint32_t u) {
 // ---- dequantization of one substep's B fragment (8 consecutive k) ----------
 __device__ __forceinline__ half8_t deq_i4_sym(uint32_t w, half_t s) {
   const half2_t sp = {s, s};
-  const half2_t bias = {(half_t)1032.f, (half_t)1032.f};
+  // A nibble in bits 0-3 of a 16-bit half merged into 0x6400 (1024.0) reads
+  // as 1024 + q; one in bits 4-7 merged into 0x5400 (64.0, whose mantissa bit
+  // 4 is worth 1) reads as 64 + q. Subtracting 1032 or 72 leaves q - 8
+  // exactly, so substeps 0/1 come from w and 2/3 from w >> 8 with one shift.
+  // The masks sit in registers so each mask-and-merge is one v_and_or_b32
+  // (its encoding takes no literal constants).
+  uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, g0 = 0x64006400u, g1 = 0x54005400u;
+  asm("" : "+v"(m0), "+v"(m1), "+v"(g0), "+v"(g1));
+  const half2_t b0 = {(half_t)1032.f, (half_t)1032.f}, b1 = {(half_t)72.f, (half_t)72.f};
+  const uint32_t w8 = w >> 8;
+  const half2_t h[4] = {(as_h2((w & m0) | g0) - b0) * sp, (as_h2((w & m1) | g1) - b1) * sp,
+                        (as_h2((w8 & m0) | g0) - b0) * sp, (as_h2((w8 & m1) | g1) - b1) * sp};
   half8_t o;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    half2_t h = as_h2(((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u);
-    h = h - bias;
-    h = h * sp;
-    o[2 * j] = h[0];
-    o[2 * j + 1] = h[1];
+    o[2 * j] = h[j][0];
+    o[2 * j + 1] = h[j][1];
   }
   return o;
 }
@@ -137,10 +145,11 @@ __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int
 }
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
                                           BRaw<TGOHIP_FORM_I4_SYM>& r) {
-  const int KS = g.K / 64;
-  const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
-  r.p = *(const uint4*)((const char*)g.wp + slot * 16);
-  r.s = *((const uint32_t*)(g.ws) + ((size_t)nb * KS + ks) * 32 + (lane & 31));
+  // (nb, ks) is uniform across the wave: a scalar base plus a 32-bit lane
+  // offset, so the loads need no 64-bit vector address arithmetic.
+  const size_t blk = (size_t)nb * (g.K / 64) + ks;
+  r.p = *(const uint4*)((const char*)g.wp + blk * 1024 + (uint32_t)lane * 16u);
+  r.s = *(const uint32_t*)((const char*)g.ws + blk * 128 + (uint32_t)(lane & 31) * 4u);
 }
 
 __device__ __forceinline__ uint32_t word_of(const uint4& p, int j) {
@@ -356,7 +365,7 @@ template <int FORM, int EPI, int MW>
 __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
   constexpr int MB = MW / 32;
   constexpr int ACH = MW / 32;  // 16-byte A chunks per thread per k-step
-  __shared__ __attribute__((aligned(16))) half_t As[2][MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As[4][MW * 64];
 
   // XCD x (workgroup b runs on XCD b % 8) owns the column tiles c = x (mod 8):
   // each weight column tile is streamed into one XCD's L2 and serves every row
@@ -366,7 +375,8 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   if (cols_x <= 0 || j >= cols_x * (tiles / tiles_n)) return;
   const int tm = j / cols_x, tn = x + 8 * (j - tm * cols_x);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   const int h = lane >> 5, c32 = lane & 31;
   const int NBT = g.N / 32;
   const int nbw0 = tn * 8 + wave * 2;
@@ -382,11 +392,11 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   // XOR-swizzled. Rows past M load row M-1 (their results are not stored).
   // (Element offsets fit 32 bits: the host checks M*K.) Chunk i sits 256
   // slots after chunk i-1 in the swizzled tile.
-  uint32_t aoff[ACH];
+  uint32_t aoff[ACH];  // byte offsets (M*K*2 < 2^32: the host checks M*K)
 #pragma unroll
   for (int i = 0; i < ACH; i++) {
     const int row = (tid >> 3) + 32 * i;
-    aoff[i] = (uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)((tid & 7) * 8);
+    aoff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)((tid & 7) * 8)) * 2u;
   }
   const int aphys0 = a_slot(tid >> 3, tid & 7);
   const half_t* xa = (const half_t*)g.x;
@@ -396,7 +406,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   // them in scratch memory across the scheduling barrier below.)
 #define PIPE_LOAD_A(ks)                                                              \
   _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
-      ra[i] = *(const u32x4_t*)(xa + aoff[i] + (uint32_t)(ks) * 64u)
+      ra[i] = *(const u32x4_t*)((const char*)(xa + (size_t)(ks) * 64) + aoff[i])
 #define PIPE_STORE_A(stage)                                                          \
   _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
       ((u32x4_t*)As[stage])[aphys0 + 256 * i] = ra[i]
@@ -409,73 +419,91 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
 
-  auto kpos = [&](int k) { return ks0 + k; };
-  if (nk > 0) {
-    const int k1 = kpos(min(1, nk - 1));
+  // A(k) sits in LDS stage k % 4, stored at the end of step k-2; B(k) in
+  // register slot k % 4, loaded at the start of step k-2. Each step reads the
+  // next step's first fragments during its last substep, so the MFMAs run on
+  // across step boundaries. One barrier per step, in its middle: a wave past
+  // the barrier of step k has finished reading A(k-1), whose stage the
+  // stores at the end of step k reuse, and has stored A(k+1), which the
+  // barrier makes visible before anyone reads it at the end of step k.
+  auto kpos = [&](int k) { return ks0 + min(k, nk - 1); };
+  half8_t afc[MB], bfc[2];
+  if (nk > 0) {  // nk is then a multiple of 4 (the host guarantees it)
     PIPE_LOAD_A(kpos(0));
 #pragma unroll
     for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(0), lane, bq[0][b]);
 #pragma unroll
-    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], k1, lane, bq[1][b]);
+    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(1), lane, bq[1][b]);
     PIPE_STORE_A(0);
+    PIPE_LOAD_A(kpos(1));
+    PIPE_STORE_A(1);
+    lds_barrier();
+    const half8_t* A = (const half8_t*)As[0];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
+#pragma unroll
+    for (int b = 0; b < 2; b++) bfc[b] = bfrag(bq[0][b], 0);
   }
-  // nk is a multiple of 4 (the host guarantees it), so the unrolled body has
-  // no conditionals and the loop carries its loads across the back edge.
   for (int kk = 0; kk < nk; kk += 4) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      {
-        // LDS stage u%2 holds A(k); stage (u+1)%2 is no longer read.
-        lds_barrier();
-        PIPE_LOAD_A(kpos(min(kk + u + 1, nk - 1)));
-        const int kn = kpos(min(kk + u + 2, nk - 1));
+      // A(k+2) is issued before B(k+2) and kept apart from it, so the wait
+      // before the store of A(k+2) leaves the B loads in flight.
+      PIPE_LOAD_A(kpos(kk + u + 2));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kn, lane, bq[(u + 2) % 4][b]);
-        // Keep the loads issued here, ahead of the MFMAs: the scheduler would
-        // otherwise sink them next to their use and expose their latency.
-        __builtin_amdgcn_sched_barrier(0);
-        const half8_t* A = (const half8_t*)As[u % 2];
-        // Substep j's MFMAs run while substep j+1's A fragments are read from
-        // LDS and its B fragments dequantized; the group barriers interleave
-        // them (1 MFMA, 1 LDS read, 5 VALU) so the matrix core stays fed.
-        half8_t afc[MB], afn[MB], bfc[2], bfn[2];
+      for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(kk + u + 2), lane, bq[(u + 2) % 4][b]);
+      // Keep the loads issued here, ahead of the MFMAs: the scheduler would
+      // otherwise sink them next to their use and expose their latency.
+      __builtin_amdgcn_sched_barrier(0);
+      const half8_t* A = (const half8_t*)As[u];
+      const half8_t* An = (const half8_t*)As[(u + 1) % 4];
+      // Substep j's MFMAs run while the next substep's A fragments are read
+      // from LDS and its B fragments dequantized; the group barriers
+      // interleave them (1 MFMA, 1 LDS read, 5 VALU) so the matrix core stays
+      // fed.
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
+      for (int j = 0; j < 4; j++) {
+        half8_t afn[MB], bfn[2];
+        if (j < 3) {
 #pragma unroll
-        for (int b = 0; b < 2; b++) bfc[b] = bfrag(bq[u % 4][b], 0);
+          for (int mb = 0; mb < MB; mb++) afn[mb] = A[a_slot(mb * 32 + c32, 2 * (j + 1) + h)];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          if (j < 3) {
+          for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[u][b], j + 1);
+        } else {
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) afn[mb] = A[a_slot(mb * 32 + c32, 2 * (j + 1) + h)];
+          for (int mb = 0; mb < MB; mb++) afn[mb] = An[a_slot(mb * 32 + c32, h)];
 #pragma unroll
-            for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[u % 4][b], j + 1);
-          }
-#pragma unroll
-          for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-            for (int b = 0; b < 2; b++)
-              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
-          if (j < 3) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-              __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-              __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
-            }
-          }
-#pragma unroll
-          for (int mb = 0; mb < MB; mb++) afc[mb] = afn[mb];
-#pragma unroll
-          for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
+          for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[(u + 1) % 4][b], 0);
         }
-        // The next A tile goes to LDS only after this step's MFMAs have been
-        // issued, so its global load had the whole step to arrive.
-        __builtin_amdgcn_sched_barrier(0);
-        PIPE_STORE_A((u + 1) % 2);
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+          for (int b = 0; b < 2; b++)
+            acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) afc[mb] = afn[mb];
+#pragma unroll
+        for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
+        if (j == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          lds_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
+      // The A tile loaded at the top of this step goes to LDS after the
+      // step's MFMAs have been issued, so its global load had the step to
+      // arrive.
+      __builtin_amdgcn_sched_barrier(0);
+      PIPE_STORE_A((u + 2) % 4);
     }
   }
   gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, gridDim.z > 1, blockIdx.z);
