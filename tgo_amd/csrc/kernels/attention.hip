@@ -180,6 +180,44 @@ __device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, ha
   }
 }
 
+// A decode wave's own 16 positions p0 + [0,16) of a tile: lane (dch, prow) =
+// (lane % 16, lane / 16) loads K positions p0 + prow + 4i and V positions
+// p0 + 4prow + i, dims 8*dch + [0,8). Positions at or past hi load zeros.
+template <int BLK>
+__device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx& c, int p0, int hi,
+                                                int prow, uint4 (&kr)[4], uint4 (&vr)[4]) {
+  if (BLK == 16 && c.staged && p0 + 16 <= hi && (p0 & 15) == 0) {
+    const uint32_t base = c.pg[(p0 >> 4) - c.pg0] * 16u;  // one whole page
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kr[i] = *(const uint4*)(a.k + (base + (uint32_t)(prow + 4 * i)) * c.rstride + c.lane_off);
+      vr[i] = *(const uint4*)(a.v + (base + (uint32_t)(4 * prow + i)) * c.rstride + c.lane_off);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int pk = p0 + prow + 4 * i, pv = p0 + 4 * prow + i;
+    kr[i] = pk < hi ? *(const uint4*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+                    : make_uint4(0, 0, 0, 0);
+    vr[i] = pv < hi ? *(const uint4*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+                    : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Writes a decode wave's block to its own LDS region (K rows swizzled as in
+// attn_store_tile, V rows at the v_off pitch). Only this wave reads it, and a
+// wave's LDS operations complete in order, so no barrier is needed.
+__device__ __forceinline__ void attn_store_block(half_t* Kw, half_t* Vw, int dch, int prow,
+                                                 const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int pk = prow + 4 * i;
+    ((uint4*)Kw)[pk * 16 + (dch ^ pk)] = kr[i];
+    *(uint4*)(Vw + v_off(4 * prow + i, 8 * dch)) = vr[i];
+  }
+}
+
 // q (f32 or f16) times scale*log2(e), split into an f16 high and low part.
 __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool valid, half8_t& hi,
                                             half8_t& lo) {
@@ -222,10 +260,12 @@ constexpr int kDecodeDepth = TGOHIP_DECODE_DEPTH;
 template <int BLK>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                             char* smem) {
-  half_t* Ks = (half_t*)smem;
-  half_t* Vs = (half_t*)(smem + 16384);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
+  // Wave w owns positions 16w + [0,16) of every tile, in an LDS region of its
+  // own: 16 K rows of 256 bytes, 16 V rows at a 320-byte pitch.
+  half_t* Kw = (half_t*)smem + wave * 16 * kHeadDim;
+  half_t* Vw = (half_t*)(smem + 16384) + wave * (kAttnVBytes / 8);
   const int G = c.G, R = it.ntok * G;
   const int r = li;
   const bool valid = r < R;
@@ -249,31 +289,29 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
   const int full_hi = min(it.kv_hi, c.L - c.n + it.tok0 + 1);
 
   constexpr int D = kDecodeDepth;
+  const int wofs = 16 * wave;
   uint4 kr[D][4], vr[D][4];
 #pragma unroll
   for (int u = 0; u < D; u++)
     if (it.kv_lo + u * kAttnTile < it.kv_hi)
-      attn_load_tile<BLK>(a, c, it.kv_lo + u * kAttnTile, it.kv_hi, kr[u], vr[u]);
+      attn_load_block<BLK>(a, c, it.kv_lo + u * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
   for (int tt = it.kv_lo; tt < it.kv_hi; tt += D * kAttnTile) {
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int t0 = tt + u * kAttnTile;
       if (t0 < it.kv_hi) {
-        attn_lds_barrier();  // the previous tile's LDS reads are done
-        attn_store_tile(c, Ks, Vs, kr[u], vr[u]);
-        attn_lds_barrier();
+        attn_store_block(Kw, Vw, li, lg, kr[u], vr[u]);
         if (t0 + D * kAttnTile < it.kv_hi)
-          attn_load_tile<BLK>(a, c, t0 + D * kAttnTile, it.kv_hi, kr[u], vr[u]);
+          attn_load_block<BLK>(a, c, t0 + D * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
 
         // Scores of this wave's 16-position block.
         const int mb = wave;
         float4_t st = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         if (t0 + mb * 16 < it.kv_hi) {
           float4_t acc = {0.f, 0.f, 0.f, 0.f};
-          const int pos = mb * 16 + li;
 #pragma unroll
           for (int cc = 0; cc < 4; cc++) {
-            const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((4 * cc + lg) ^ (pos & 15))) * 8);
+            const half8_t ka = *(const half8_t*)(Kw + (li * 16 + ((4 * cc + lg) ^ li)) * 8);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[cc], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[cc], acc, 0, 0, 0);
           }
@@ -311,7 +349,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           // O^T += V^T . P^T; the A operand is V^T[dim 16db+li][pos 16mb+4lg..+3].
 #pragma unroll
           for (int db = 0; db < 8; db++) {
-            const half4_t va = attn_vt4(Vs, mb * 16 + 4 * lg, db * 16, li);
+            const half4_t va = attn_vt4(Vw, 4 * lg, db * 16, li);
             o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[db], 0, 0, 0);
           }
         }
