@@ -253,6 +253,15 @@ __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool 
 #endif
 constexpr int kDecodeDepth = TGOHIP_DECODE_DEPTH;
 
+// Online softmax with a lazy reference maximum: a row's m starts at kNoMax (a
+// finite "nothing seen", so masked scores of -inf give exp2 = 0 without a
+// select) and moves only when a tile's maximum exceeds it by more than
+// kLazyMax (log2 units). Probabilities then stay below 2^kLazyMax, well inside
+// f16, and most tiles skip rescaling the accumulators; the result is the same
+// softmax, normalised by a sum taken against the same m.
+constexpr float kNoMax = -1.0e30f;
+constexpr float kLazyMax = 8.f;
+
 // Decode-style item (at most 16 rows: the G query heads of <= 16/G tokens).
 // The four waves take the four 16-position blocks of each 64-position tile and
 // merge their softmax states at the end. kDecodeDepth tiles of loads are in
@@ -282,7 +291,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
     for (int cc = 0; cc < 4; cc++) attn_load_q(a, qoff + 32 * cc + 8 * lg, valid, qh[cc], ql[cc]);
   }
 
-  float m = -INFINITY, l = 0.f;
+  float m = kNoMax, l = 0.f;
   float4_t o[8];
 #pragma unroll
   for (int db = 0; db < 8; db++) o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -327,24 +336,27 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
         }
         float tmax = fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3]));
         tmax = wave_max16x(tmax);
-        // Branch-free update: a row that has seen no visible position keeps
-        // m = -inf, alpha = 1 and p = 0. The MFMAs below run on every lane.
-        const float mnew = fmaxf(m, tmax);
-        const bool none = mnew == -INFINITY;
-        const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+        // A row that has seen no visible position keeps m = kNoMax and gets
+        // p = 0. The MFMAs below run on every lane.
+        const bool grow = tmax > m + kLazyMax;
+        if (__builtin_amdgcn_ballot_w64(grow)) {  // uniform across the wave
+          const float mnew = grow ? tmax : m;
+          const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+          l *= alpha;
+#pragma unroll
+          for (int db = 0; db < 8; db++) o[db] *= alpha;
+          m = mnew;
+        }
         float psum = 0.f;
         half4_t pb;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const float p = none ? 0.f : __builtin_amdgcn_exp2f(st[q] - mnew);
+          const float p = __builtin_amdgcn_exp2f(st[q] - m);
           psum += p;
           pb[q] = (half_t)p;
         }
         psum = wave_sum16x(psum);
-        l = l * alpha + psum;
-        m = mnew;
-#pragma unroll
-        for (int db = 0; db < 8; db++) o[db] *= alpha;
+        l += psum;
         if (t0 + mb * 16 < it.kv_hi) {
           // O^T += V^T . P^T; the A operand is V^T[dim 16db+li][pos 16mb+4lg..+3].
 #pragma unroll
@@ -367,7 +379,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
 #pragma unroll
   for (int db = 0; db < 8; db++) *(float4_t*)(Os + (wave * 16 + li) * kOs + db * 16 + 4 * lg) = o[db];
   if (lg == 0) {
-    Ms[wave * 16 + li] = m;
+    Ms[wave * 16 + li] = l > 0.f ? m : -INFINITY;
     Ms[64 + wave * 16 + li] = l;
   }
   attn_lds_barrier();
@@ -445,7 +457,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
     for (int ss = 0; ss < 8; ss++) attn_load_q(a, qoff + 16 * ss + 8 * kh, valid, qh[ss], ql[ss]);
   }
 
-  float m = -INFINITY, l = 0.f;
+  float m = kNoMax, l = 0.f;
   float16_t o[4];
 #pragma unroll
   for (int db = 0; db < 4; db++)
@@ -491,24 +503,27 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
         }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(m, tmax);
-    const bool none = mnew == -INFINITY;
-    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+    const bool grow = tmax > m + kLazyMax;
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // uniform across the wave
+      const float mnew = grow ? tmax : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; db++) o[db] *= alpha;
+      m = mnew;
+    }
     float psum = 0.f;
     half8_t pf[2][2];
 #pragma unroll
     for (int pb = 0; pb < 2; pb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float p = none ? 0.f : __builtin_amdgcn_exp2f(sc[pb][i] - mnew);
+        const float p = __builtin_amdgcn_exp2f(sc[pb][i] - m);
         psum += p;
         pf[pb][i >> 3][i & 7] = (half_t)p;
       }
     psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-    m = mnew;
-#pragma unroll
-    for (int db = 0; db < 4; db++) o[db] *= alpha;
+    l += psum;
     // The PV operand of lane (l32, kh): dim 32db + l32, positions
     // 32pb + 16t + 4kh + [0,4) and the same + 8 -- two transposing reads whose
     // 16-lane groups take dims 32db + 16*(l32/16) + [0,16).
@@ -559,7 +574,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
         *(float4_t*)(po + db * 32 + 8 * g + 4 * kh) = fv;
       }
     if (kh == 0) {
-      a.part_ml[(size_t)it.part * 2 * kAttnRowsP + r] = m;
+      a.part_ml[(size_t)it.part * 2 * kAttnRowsP + r] = l > 0.f ? m : -INFINITY;
       a.part_ml[(size_t)it.part * 2 * kAttnRowsP + kAttnRowsP + r] = l;
     }
   }
