@@ -104,6 +104,8 @@ typedef struct {
 } tgohip_model_cfg;
 
 int tgohip_config(tgohip_ctx* ctx, const tgohip_model_cfg* cfg);
+/* The configuration a context was given (for a loader that walks its ports). */
+int tgohip_get_config(tgohip_ctx* ctx, tgohip_model_cfg* cfg);
 
 /* Uploads one weight port, as nn.Graph.Weight declares it (nn/nn.go:209-259)
  * and weights.Load binds it (weights/weights.go:629-743, model.go:489-543).
@@ -303,6 +305,58 @@ void tgohip_quantize_int8(const float* src, size_t n, int8_t* q, uint16_t* scale
 /* int4 asymmetric quantizer in the I4_TGO layout (weights/weights.go:694-743). */
 void tgohip_quantize_int4(const float* src, size_t n, uint32_t* codes, uint16_t* scales,
                           uint16_t* zeros);
+
+/* ---- checkpoint loading: safetensors/, weights/weights.go, model/qwen3.go -- */
+typedef struct tgohip_st tgohip_st;
+typedef struct tgohip_repo tgohip_repo;
+/* Opens one safetensors file and validates its header as hostile input, as
+ * safetensors.Open does (safetensors/safetensors.go:116-277): the length
+ * prefix fits the file and a 100 MiB cap; the header is a JSON object; every
+ * entry has a known dtype, two data_offsets inside the data region, no
+ * negative dimension, an element count that does not overflow and that
+ * matches the byte span; no two tensors share a byte; __metadata__ is a map
+ * of strings. Entries are validated and kept in name order. NULL on refusal;
+ * tgohip_last_error() names the tensor in the reference's words. */
+tgohip_st* tgohip_st_open(const char* path);
+void tgohip_st_close(tgohip_st* f);
+int tgohip_st_count(const tgohip_st* f);
+/* Entry i in name order (File.Names/Entry, safetensors.go:283-301): the name
+ * and dtype strings live as long as f; up to 8 dimensions; the byte span is
+ * relative to the end of the header. */
+int tgohip_st_entry(const tgohip_st* f, int i, const char** name, const char** dtype, int* rank,
+                    int64_t* shape, int64_t* begin, int64_t* end);
+/* A tensor's raw bytes (File.Bytes, safetensors.go:302-323); returns the count. */
+int64_t tgohip_st_read(const tgohip_st* f, const char* name, void* dst, int64_t cap);
+/* Lowers the header cap (0 restores 100 MiB); the reference's tests lower it
+ * the same way (safetensors_test.go:283-292). */
+void tgohip_st_set_max_header(int64_t bytes);
+/* A model directory (safetensors.OpenRepo, safetensors/repo.go:48-196): one
+ * model.safetensors, or the shards model.safetensors.index.json names, checked
+ * both ways (every indexed tensor is in its shard, every shard tensor is
+ * indexed to it); shard names are plain file names; a config.json, when
+ * present, is valid JSON. */
+tgohip_repo* tgohip_repo_open(const char* dir);
+void tgohip_repo_close(tgohip_repo* r);
+int tgohip_repo_has(const tgohip_repo* r, const char* name);
+/* The f32 plane of a tensor after the loader's conversions (convertOne,
+ * weights/weights.go:552-627; convert.go:41-131): BF16 widened by a 16-bit
+ * shift, F16 exactly, F32 as stored (other dtypes refused); [rows, cols]
+ * transposed to [cols, rows] when transpose; then, when head_dim > 0, each
+ * head_dim segment of the last axis re-paired y[2i] = x[i],
+ * y[2i+1] = x[i + head_dim/2]. n is the element count of out. */
+int tgohip_repo_plane(const tgohip_repo* r, const char* name, int transpose, int head_dim,
+                      float* out, int64_t n);
+/* weights.Load for a configured Qwen3 context (model/qwen3.go:54-205;
+ * weights/weights.go:378-627): every port of the weight map, each tensor
+ * present with the shape the config declares before any is converted, then
+ * one at a time: plane as above (q/k projections and q/k-norm gains permuted,
+ * projections and the head transposed), then form F16 (saturation over 1e-5
+ * of a tensor refused), I8 or I4_TGO, uploaded through tgohip_weight /
+ * tgohip_gain. The gathered embedding is capped at I8 under int4. tie: the
+ * config's tie_word_embeddings -- the head is then the embedding tensor
+ * transposed, and a checkpoint that also ships lm_head.weight is refused.
+ * saturated (optional) receives the f16 saturation count. */
+int tgohip_load_qwen3(tgohip_ctx* ctx, const tgohip_repo* r, int form, int tie, int64_t* saturated);
 
 #ifdef __cplusplus
 }

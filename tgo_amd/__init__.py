@@ -118,6 +118,20 @@ def lib():
         "tgohip_to_f16": (ctypes.c_size_t, [P, P, ctypes.c_size_t]),
         "tgohip_quantize_int8": (None, [P, ctypes.c_size_t, P, P]),
         "tgohip_quantize_int4": (None, [P, ctypes.c_size_t, P, P, P]),
+        "tgohip_get_config": (I, [P, ctypes.POINTER(ModelCfg)]),
+        "tgohip_st_open": (P, [ctypes.c_char_p]),
+        "tgohip_st_close": (None, [P]),
+        "tgohip_st_count": (I, [P]),
+        "tgohip_st_entry": (I, [P, I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
+                                ctypes.POINTER(ctypes.c_int), P, ctypes.POINTER(ctypes.c_int64),
+                                ctypes.POINTER(ctypes.c_int64)]),
+        "tgohip_st_read": (ctypes.c_int64, [P, ctypes.c_char_p, P, ctypes.c_int64]),
+        "tgohip_st_set_max_header": (None, [ctypes.c_int64]),
+        "tgohip_repo_open": (P, [ctypes.c_char_p]),
+        "tgohip_repo_close": (None, [P]),
+        "tgohip_repo_has": (I, [P, ctypes.c_char_p]),
+        "tgohip_repo_plane": (I, [P, ctypes.c_char_p, I, I, P, ctypes.c_int64]),
+        "tgohip_load_qwen3": (I, [P, P, I, I, ctypes.POINTER(ctypes.c_int64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -313,6 +327,82 @@ def quantize_int4(w):
 # device context
 # ---------------------------------------------------------------------------
 
+class SafeTensors:
+    """safetensors.File (safetensors/safetensors.go): a validated header, planes on demand."""
+
+    def __init__(self, path):
+        self.h = lib().tgohip_st_open(os.fsencode(path))
+        if not self.h:
+            raise TgoError(EINVAL, last_error())
+
+    def close(self):
+        if self.h:
+            lib().tgohip_st_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def entries(self):
+        """-> {name: (dtype, shape tuple, begin, end)} in name order."""
+        out = {}
+        for i in range(lib().tgohip_st_count(self.h)):
+            nm, dt = ctypes.c_char_p(), ctypes.c_char_p()
+            rank = ctypes.c_int()
+            shape = np.zeros(8, np.int64)
+            b, e = ctypes.c_int64(), ctypes.c_int64()
+            check(lib().tgohip_st_entry(self.h, i, ctypes.byref(nm), ctypes.byref(dt),
+                                        ctypes.byref(rank), ptr(shape), ctypes.byref(b),
+                                        ctypes.byref(e)))
+            out[nm.value.decode()] = (dt.value.decode(), tuple(int(x) for x in shape[:rank.value]),
+                                      b.value, e.value)
+        return out
+
+    def read(self, name):
+        ent = self.entries()
+        n = ent[name][3] - ent[name][2] if name in ent else 0
+        buf = np.zeros(max(n, 1), np.uint8)
+        got = check(lib().tgohip_st_read(self.h, name.encode(), ptr(buf), n))
+        return buf[:got].tobytes()
+
+
+def set_safetensors_header_cap(nbytes):
+    """Lowers the header-length cap (0 restores 100 MiB)."""
+    lib().tgohip_st_set_max_header(nbytes)
+
+
+class Repo:
+    """safetensors.Repo (safetensors/repo.go): one model directory, single or sharded."""
+
+    def __init__(self, path):
+        self.h = lib().tgohip_repo_open(os.fsencode(path))
+        if not self.h:
+            raise TgoError(EINVAL, last_error())
+
+    def close(self):
+        if self.h:
+            lib().tgohip_repo_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def has(self, name):
+        return bool(lib().tgohip_repo_has(self.h, name.encode()))
+
+    def plane(self, name, n, transpose=False, head_dim=0):
+        """The loader's f32 plane of `name` (decode, transpose, head permutation)."""
+        out = np.zeros(n, np.float32)
+        check(lib().tgohip_repo_plane(self.h, name.encode(), int(transpose), head_dim, ptr(out), n))
+        return out
+
+
 class Context:
     """One device, one stream: accel.Device + Queue for the batched path."""
 
@@ -371,6 +461,12 @@ class Context:
     def gain(self, port, g):
         g = np.ascontiguousarray(g, dtype=np.float32)
         check(lib().tgohip_gain(self.h, port.encode(), ptr(g), g.size))
+
+    def load_qwen3(self, repo, form, tie=False):
+        """weights.Load of every Qwen3 port from `repo`; returns the f16 saturation count."""
+        sat = ctypes.c_int64()
+        check(lib().tgohip_load_qwen3(self.h, repo.h, form, int(tie), ctypes.byref(sat)))
+        return sat.value
 
     def synth_weights(self, seed, form, sigma):
         check(lib().tgohip_synth_weights(self.h, seed, form, sigma))

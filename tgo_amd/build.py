@@ -14,7 +14,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_SOURCES = ["runtime.hip", "kernels/attention.hip", "kernels/gemm.hip",
                "kernels/elementwise.hip"]
-CXX_SOURCES = ["host/hostlogic.cpp"]
+CXX_SOURCES = ["host/hostlogic.cpp", "host/checkpoint.cpp"]
 
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
              "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-lambda-capture",

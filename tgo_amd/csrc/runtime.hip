@@ -528,6 +528,12 @@ int tgohip_config(tgohip_ctx* c, const tgohip_model_cfg* m) {
   return 0;
 }
 
+int tgohip_get_config(tgohip_ctx* c, tgohip_model_cfg* out) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "config: the context is not configured");
+  *out = c->cfg;
+  return 0;
+}
+
 int tgohip_weight(tgohip_ctx* c, const char* port, int form, int K, int N, const void* plane,
                   const void* scales, const void* zeros) {
   if (!c->configured) return fail(TGOHIP_ESTATE, "weight: configure the context first");
