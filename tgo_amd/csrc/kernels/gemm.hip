@@ -456,6 +456,10 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
       // Keep the loads issued here, ahead of the MFMAs: the scheduler would
       // otherwise sink them next to their use and expose their latency.
       __builtin_amdgcn_sched_barrier(0);
+      // Raised wave priority through the MFMA phase: of the two waves sharing
+      // a SIMD, the one issuing MFMAs goes first, the other's loads and
+      // stores fill the gaps.
+      __builtin_amdgcn_s_setprio(1);
       const half8_t* A = (const half8_t*)As[u];
       const half8_t* An = (const half8_t*)As[(u + 1) % 4];
       // Substep j's MFMAs run while the next substep's A fragments are read
@@ -503,6 +507,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
       // step's MFMAs have been issued, so its global load had the step to
       // arrive.
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
       PIPE_STORE_A((u + 2) % 4);
     }
   }
