@@ -612,8 +612,14 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   c.pgrp = tid >> 4;
   c.lane_off = (uint32_t)c.kvh * kHeadDim + c.dch * 8;
   __syncthreads();  // pg visible
-  if (it.mode == 0) attn_decode<BLK>(a, it, c, smem);
-  else attn_prefill<BLK>(a, it, c, smem);
+  if (it.mode == 0) {
+    // Decode waves are HBM streams: raised priority lets their loads and short
+    // softmax steps issue ahead of a co-resident prefill item's MFMA work.
+    __builtin_amdgcn_s_setprio(1);
+    attn_decode<BLK>(a, it, c, smem);
+  } else {
+    attn_prefill<BLK>(a, it, c, smem);
+  }
 }
 
 // Merges the parts of split items in part order (deterministic). A block
