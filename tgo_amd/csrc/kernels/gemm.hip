@@ -20,10 +20,12 @@
 //
 // Tiling: 256 threads = 4 waves side by side in N; a workgroup owns MW rows x
 // 256 columns; each wave MW x 64 (MW/32 x 2 MFMA blocks of 32x32). The
-// activation tile (MW x 64 f16) is double-buffered in LDS, XOR-swizzled. An f32
-// activation is carried as f16 hi + lo (two MFMAs) so the product keeps ~22
-// bits of the activation. Split-K over grid.z writes f32 partials that a
-// reduction kernel sums in split order (deterministic) and finishes.
+// activation tile (MW x 64 f16) is staged in LDS, XOR-swizzled: double-buffered
+// through registers in gemm_kernel, a four-stage ring filled by LDS DMA in
+// gemm_pipe_kernel. An f32 activation is carried as f16 hi + lo (two MFMAs) so
+// the product keeps ~22 bits of the activation. Split-K over grid.z writes f32
+// partials that a reduction kernel (or the consumer) sums in split order
+// (deterministic).
 #include "../common.h"
 
 #include <algorithm>
@@ -364,8 +366,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 template <int FORM, int EPI, int MW>
 __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
   constexpr int MB = MW / 32;
-  constexpr int ACH = MW / 32;  // 16-byte A chunks per thread per k-step
-  __shared__ __attribute__((aligned(16))) half_t As[4][MW * 64];
+  constexpr int ACH = MW / 32;  // 1 KiB LDS-DMA chunks per wave per k-step
+  // Four LDS stages, separate arrays so the compiler can tell a DMA into one
+  // stage from reads of another.
+  __shared__ __attribute__((aligned(16))) half_t As0[MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As1[MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As2[MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As3[MW * 64];
+  half_t* const As[4] = {As0, As1, As2, As3};
 
   // XCD x (workgroup b runs on XCD b % 8) owns the column tiles c = x (mod 8):
   // each weight column tile is streamed into one XCD's L2 and serves every row
@@ -388,28 +396,24 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   // Out-of-range column blocks load a valid block (results are not stored).
   const int nbl[2] = {min(nbw0, NBT - 1), min(nbw0 + 1, NBT - 1)};
 
-  // Chunk c = tid + 256 i of the A tile: row c/8, k-chunk c%8, stored
-  // XOR-swizzled. Rows past M load row M-1 (their results are not stored).
-  // (Element offsets fit 32 bits: the host checks M*K.) Chunk i sits 256
-  // slots after chunk i-1 in the swizzled tile.
-  uint32_t aoff[ACH];  // byte offsets (M*K*2 < 2^32: the host checks M*K)
+  // The A tile goes global -> LDS by DMA (global_load_lds_dwordx4): lane l of
+  // wave w's chunk i writes the 16-byte slot p = (4i + w)*64 + l, which holds
+  // (row p/8, k-chunk (p%8) ^ ((row/2)%8)) of the swizzled tile. Rows past M
+  // load row M-1 (their results are not stored). Byte offsets fit 32 bits:
+  // the host checks M*K.
+  uint32_t doff[ACH];
 #pragma unroll
   for (int i = 0; i < ACH; i++) {
-    const int row = (tid >> 3) + 32 * i;
-    aoff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)((tid & 7) * 8)) * 2u;
+    const int p = (4 * i + wave) * 64 + lane, row = p >> 3, kc = (p & 7) ^ ((row >> 1) & 7);
+    doff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)(kc * 8)) * 2u;
   }
-  const int aphys0 = a_slot(tid >> 3, tid & 7);
-  const half_t* xa = (const half_t*)g.x;
-  u32x4_t ra[ACH];
+  const char* xa = (const char*)g.x;
   BRaw<FORM> bq[4][2];  // B(k) in slot k % 4; three are live at a time
-  // (No lambdas over ra/bq here: a closure holding their addresses would keep
-  // them in scratch memory across the scheduling barrier below.)
-#define PIPE_LOAD_A(ks)                                                              \
-  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
-      ra[i] = *(const u32x4_t*)((const char*)(xa + (size_t)(ks) * 64) + aoff[i])
-#define PIPE_STORE_A(stage)                                                          \
-  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
-      ((u32x4_t*)As[stage])[aphys0 + 256 * i] = ra[i]
+#define PIPE_DMA_A(ks, stage)                                                          \
+  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                      \
+      __builtin_amdgcn_global_load_lds(                                                \
+          (const __attribute__((address_space(1))) void*)(xa + (size_t)(ks) * 128 + doff[i]), \
+          (__attribute__((address_space(3))) void*)(As[stage] + (4 * i + wave) * 512), 16, 0, 0)
 
   float16_t acc[MB][2];
 #pragma unroll
@@ -419,25 +423,30 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
 
-  // A(k) sits in LDS stage k % 4, stored at the end of step k-2; B(k) in
+  // A(k) sits in LDS stage k % 4, DMA'd in the middle of step k-3; B(k) in
   // register slot k % 4, loaded at the start of step k-2. Each step reads the
   // next step's first fragments during its last substep, so the MFMAs run on
-  // across step boundaries. One barrier per step, in its middle: a wave past
-  // the barrier of step k has finished reading A(k-1), whose stage the
-  // stores at the end of step k reuse, and has stored A(k+1), which the
-  // barrier makes visible before anyone reads it at the end of step k.
+  // across step boundaries. One barrier per step, in its middle. Before it a
+  // wave waits for its own DMA of A(k+1) (issued at step k-2: the vector
+  // memory operations issued since are B(k), A(k+2)'s DMA and B(k+1), so
+  // vmcnt <= 8 + ACH) and for its LDS reads; past it, A(k+1) is visible to
+  // every wave, and every wave is done reading A(k-1), whose stage the DMA of
+  // A(k+3) issued right after the barrier reuses. The barrier carries no
+  // memory fence: a fence would wait for every DMA in flight.
   auto kpos = [&](int k) { return ks0 + min(k, nk - 1); };
   half8_t afc[MB], bfc[2];
   if (nk > 0) {  // nk is then a multiple of 4 (the host guarantees it)
-    PIPE_LOAD_A(kpos(0));
 #pragma unroll
     for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(0), lane, bq[0][b]);
 #pragma unroll
     for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(1), lane, bq[1][b]);
-    PIPE_STORE_A(0);
-    PIPE_LOAD_A(kpos(1));
-    PIPE_STORE_A(1);
-    lds_barrier();
+    PIPE_DMA_A(kpos(0), 0);
+    PIPE_DMA_A(kpos(1), 1);
+    PIPE_DMA_A(kpos(2), 2);
+    __builtin_amdgcn_s_waitcnt(0);  // all counters: the prologue's loads and DMA
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     const half8_t* A = (const half8_t*)As[0];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
@@ -447,18 +456,13 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   for (int kk = 0; kk < nk; kk += 4) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      // A(k+2) is issued before B(k+2) and kept apart from it, so the wait
-      // before the store of A(k+2) leaves the B loads in flight.
-      PIPE_LOAD_A(kpos(kk + u + 2));
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(kk + u + 2), lane, bq[(u + 2) % 4][b]);
       // Keep the loads issued here, ahead of the MFMAs: the scheduler would
       // otherwise sink them next to their use and expose their latency.
       __builtin_amdgcn_sched_barrier(0);
       // Raised wave priority through the MFMA phase: of the two waves sharing
-      // a SIMD, the one issuing MFMAs goes first, the other's loads and
-      // stores fill the gaps.
+      // a SIMD, the one issuing MFMAs goes first.
       __builtin_amdgcn_s_setprio(1);
       const half8_t* A = (const half8_t*)As[u];
       const half8_t* An = (const half8_t*)As[(u + 1) % 4];
@@ -499,21 +503,22 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
         for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
         if (j == 1) {
           __builtin_amdgcn_sched_barrier(0);
-          lds_barrier();
+          // vmcnt(8 + ACH), expcnt untouched, lgkmcnt(0)
+          __builtin_amdgcn_s_waitcnt((8 + ACH) | (7 << 4));
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          PIPE_DMA_A(kpos(kk + u + 3), (u + 3) % 4);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // The A tile loaded at the top of this step goes to LDS after the
-      // step's MFMAs have been issued, so its global load had the step to
-      // arrive.
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
-      PIPE_STORE_A((u + 2) % 4);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no DMA into LDS outlives the loop
   gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, gridDim.z > 1, blockIdx.z);
-#undef PIPE_LOAD_A
-#undef PIPE_STORE_A
+#undef PIPE_DMA_A
 }
 
 // Sums split-K partials in split order and applies the epilogue.
