@@ -363,6 +363,61 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 // activations, mostly L2-resident) is issued at step j-1 and written to a
 // double-buffered LDS tile at the end of that step. Barriers order LDS only, so
 // loads stay in flight across them.
+// ---- the pipelined kernel's B operand per form ------------------------------
+// The register part of one (column block, k-step) of B. For int8 and tgo's
+// int4 the per-k scales (and zeros) are the same for the 32 columns of a
+// block, so they travel by LDS DMA with the activation tile instead of in
+// registers (8 scale/zero pairs per lane per substep would not fit).
+template <int FORM> struct PipeB;
+template <> struct PipeB<TGOHIP_FORM_I4_SYM> { uint4 p; uint32_t s; };
+template <> struct PipeB<TGOHIP_FORM_I4_TGO> { uint4 p; };
+template <> struct PipeB<TGOHIP_FORM_I8> { uint4 p[2]; };
+
+template <int FORM> constexpr bool pipe_lds_scales() { return FORM != TGOHIP_FORM_I4_SYM; }
+// Vector memory instructions a wave issues per k-step for its two B blocks.
+template <int FORM> constexpr int pipe_b_loads() { return FORM == TGOHIP_FORM_I4_TGO ? 2 : 4; }
+
+__device__ __forceinline__ void load_pipeb(const GemmArgs& g, int nb, int ks, int lane,
+                                           PipeB<TGOHIP_FORM_I4_SYM>& r) {
+  BRaw<TGOHIP_FORM_I4_SYM> b;
+  load_braw(g, nb, ks, lane, b);
+  r.p = b.p;
+  r.s = b.s;
+}
+__device__ __forceinline__ void load_pipeb(const GemmArgs& g, int nb, int ks, int lane,
+                                           PipeB<TGOHIP_FORM_I4_TGO>& r) {
+  const size_t blk = (size_t)nb * (g.K / 64) + ks;
+  r.p = *(const uint4*)((const char*)g.wp + blk * 1024 + (uint32_t)lane * 16u);
+}
+__device__ __forceinline__ void load_pipeb(const GemmArgs& g, int nb, int ks, int lane,
+                                           PipeB<TGOHIP_FORM_I8>& r) {
+  const size_t blk = (size_t)nb * (g.K / 64) + ks;
+  const uint4* pp = (const uint4*)((const char*)g.wp + blk * 2048 + (uint32_t)lane * 32u);
+  r.p[0] = pp[0];
+  r.p[1] = pp[1];
+}
+// Substep j's B fragment. sz: this wave's scale region of the k-step's stage
+// (scales of block b at b*64 + (2j + h)*8, zeros 128 halves further).
+__device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I4_SYM>& r, int j,
+                                              const half_t* sz, int b, int h) {
+  BRaw<TGOHIP_FORM_I4_SYM> x;
+  x.p = r.p;
+  x.s = r.s;
+  return bfrag(x, j);
+}
+__device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I4_TGO>& r, int j,
+                                              const half_t* sz, int b, int h) {
+  const half8_t s8 = *(const half8_t*)(sz + b * 64 + (2 * j + h) * 8);
+  const half8_t z8 = *(const half8_t*)(sz + 128 + b * 64 + (2 * j + h) * 8);
+  return deq_i4_asym(word_of(r.p, j), s8, z8);
+}
+__device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I8>& r, int j,
+                                              const half_t* sz, int b, int h) {
+  const half8_t s8 = *(const half8_t*)(sz + b * 64 + (2 * j + h) * 8);
+  const uint4 q = r.p[j >> 1];
+  return deq_i8((j & 1) ? q.z : q.x, (j & 1) ? q.w : q.y, s8);
+}
+
 template <int FORM, int EPI, int MW>
 __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
   constexpr int MB = MW / 32;
@@ -374,6 +429,14 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   __shared__ __attribute__((aligned(16))) half_t As2[MW * 64];
   __shared__ __attribute__((aligned(16))) half_t As3[MW * 64];
   half_t* const As[4] = {As0, As1, As2, As3};
+  // Per-stage scales and zeros of the four waves' column blocks (int8, tgo int4).
+  constexpr bool LS = pipe_lds_scales<FORM>();
+  constexpr int SZN = LS ? 4 * 256 : 8;
+  __shared__ __attribute__((aligned(16))) half_t Sz0[SZN];
+  __shared__ __attribute__((aligned(16))) half_t Sz1[SZN];
+  __shared__ __attribute__((aligned(16))) half_t Sz2[SZN];
+  __shared__ __attribute__((aligned(16))) half_t Sz3[SZN];
+  half_t* const Sz[4] = {Sz0, Sz1, Sz2, Sz3};
 
   // XCD x (workgroup b runs on XCD b % 8) owns the column tiles c = x (mod 8):
   // each weight column tile is streamed into one XCD's L2 and serves every row
@@ -408,12 +471,24 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
     doff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)(kc * 8)) * 2u;
   }
   const char* xa = (const char*)g.x;
-  BRaw<FORM> bq[4][2];  // B(k) in slot k % 4; three are live at a time
+  PipeB<FORM> bq[4][2];  // B(k) in slot k % 4; three are live at a time
+  // A wave's scales (lanes 0-15: blocks nbl[0], nbl[1]) and zeros (lanes
+  // 16-31) of one k-step are 128-byte runs of the packed arrays.
+  const int szl = lane & 15, szb = szl >> 3;
+  const char* szsrc = (const char*)((lane >> 4) ? g.wz : g.ws) +
+                      ((size_t)nbl[szb] * KS * 64 + (size_t)(szl & 7) * 8) * 2;
+  const bool szlane = LS && (lane < (FORM == TGOHIP_FORM_I4_TGO ? 32 : 16));
 #define PIPE_DMA_A(ks, stage)                                                          \
-  _Pragma("unroll") for (int i = 0; i < ACH; i++)                                      \
+  do {                                                                                 \
+    _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
+        __builtin_amdgcn_global_load_lds(                                              \
+            (const __attribute__((address_space(1))) void*)(xa + (size_t)(ks) * 128 + doff[i]), \
+            (__attribute__((address_space(3))) void*)(As[stage] + (4 * i + wave) * 512), 16, 0, 0); \
+    if (LS && szlane)                                                                  \
       __builtin_amdgcn_global_load_lds(                                                \
-          (const __attribute__((address_space(1))) void*)(xa + (size_t)(ks) * 128 + doff[i]), \
-          (__attribute__((address_space(3))) void*)(As[stage] + (4 * i + wave) * 512), 16, 0, 0)
+          (const __attribute__((address_space(1))) void*)(szsrc + (size_t)(ks) * 128), \
+          (__attribute__((address_space(3))) void*)(Sz[stage] + wave * 256), 16, 0, 0); \
+  } while (0)
 
   float16_t acc[MB][2];
 #pragma unroll
@@ -423,23 +498,24 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
 
-  // A(k) sits in LDS stage k % 4, DMA'd in the middle of step k-3; B(k) in
-  // register slot k % 4, loaded at the start of step k-2. Each step reads the
-  // next step's first fragments during its last substep, so the MFMAs run on
-  // across step boundaries. One barrier per step, in its middle. Before it a
-  // wave waits for its own DMA of A(k+1) (issued at step k-2: the vector
-  // memory operations issued since are B(k), A(k+2)'s DMA and B(k+1), so
-  // vmcnt <= 8 + ACH) and for its LDS reads; past it, A(k+1) is visible to
-  // every wave, and every wave is done reading A(k-1), whose stage the DMA of
-  // A(k+3) issued right after the barrier reuses. The barrier carries no
-  // memory fence: a fence would wait for every DMA in flight.
+  // A(k) (and the scales of B(k) when they travel by LDS) sits in LDS stage
+  // k % 4, DMA'd in the middle of step k-3; B(k) in register slot k % 4,
+  // loaded at the start of step k-2. Each step reads the next step's first
+  // fragments during its last substep, so the MFMAs run on across step
+  // boundaries. One barrier per step, in its middle. Before it a wave waits
+  // for its own DMA of stage k+1 (issued at step k-2: the vector memory
+  // operations issued since are B(k), stage k+2's DMA and B(k+1)) and for its
+  // LDS reads; past it, stage k+1 is visible to every wave, and every wave is
+  // done reading stage k-1, which the DMA of stage k+3 issued right after the
+  // barrier reuses. The barrier carries no memory fence: a fence would wait
+  // for every DMA in flight.
   auto kpos = [&](int k) { return ks0 + min(k, nk - 1); };
   half8_t afc[MB], bfc[2];
   if (nk > 0) {  // nk is then a multiple of 4 (the host guarantees it)
 #pragma unroll
-    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(0), lane, bq[0][b]);
+    for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(0), lane, bq[0][b]);
 #pragma unroll
-    for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(1), lane, bq[1][b]);
+    for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(1), lane, bq[1][b]);
     PIPE_DMA_A(kpos(0), 0);
     PIPE_DMA_A(kpos(1), 1);
     PIPE_DMA_A(kpos(2), 2);
@@ -451,13 +527,13 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
 #pragma unroll
-    for (int b = 0; b < 2; b++) bfc[b] = bfrag(bq[0][b], 0);
+    for (int b = 0; b < 2; b++) bfc[b] = pipe_bfrag(bq[0][b], 0, Sz[0] + wave * 256, b, h);
   }
   for (int kk = 0; kk < nk; kk += 4) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
 #pragma unroll
-      for (int b = 0; b < 2; b++) load_braw(g, nbl[b], kpos(kk + u + 2), lane, bq[(u + 2) % 4][b]);
+      for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(kk + u + 2), lane, bq[(u + 2) % 4][b]);
       // Keep the loads issued here, ahead of the MFMAs: the scheduler would
       // otherwise sink them next to their use and expose their latency.
       __builtin_amdgcn_sched_barrier(0);
@@ -477,12 +553,13 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
 #pragma unroll
           for (int mb = 0; mb < MB; mb++) afn[mb] = A[a_slot(mb * 32 + c32, 2 * (j + 1) + h)];
 #pragma unroll
-          for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[u][b], j + 1);
+          for (int b = 0; b < 2; b++) bfn[b] = pipe_bfrag(bq[u][b], j + 1, Sz[u] + wave * 256, b, h);
         } else {
 #pragma unroll
           for (int mb = 0; mb < MB; mb++) afn[mb] = An[a_slot(mb * 32 + c32, h)];
 #pragma unroll
-          for (int b = 0; b < 2; b++) bfn[b] = bfrag(bq[(u + 1) % 4][b], 0);
+          for (int b = 0; b < 2; b++)
+            bfn[b] = pipe_bfrag(bq[(u + 1) % 4][b], 0, Sz[(u + 1) % 4] + wave * 256, b, h);
         }
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
@@ -503,8 +580,8 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
         for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
         if (j == 1) {
           __builtin_amdgcn_sched_barrier(0);
-          // vmcnt(8 + ACH), expcnt untouched, lgkmcnt(0)
-          __builtin_amdgcn_s_waitcnt((8 + ACH) | (7 << 4));
+          // vmcnt(2 * B loads + A DMA + scale DMA), expcnt untouched, lgkmcnt(0)
+          __builtin_amdgcn_s_waitcnt((2 * pipe_b_loads<FORM>() + ACH + (LS ? 1 : 0)) | (7 << 4));
           asm volatile("" ::: "memory");
           __builtin_amdgcn_s_barrier();
           asm volatile("" ::: "memory");
@@ -854,8 +931,20 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
     g.part = workspace;
   }
   const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
-  if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_SYM, 128>(g, epi, grid, tiles_n, tiles, st);
-  else launch_pipe_form<TGOHIP_FORM_I4_SYM, 64>(g, epi, grid, tiles_n, tiles, st);
+  switch (w.form) {
+    case TGOHIP_FORM_I4_SYM:
+      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_SYM, 128>(g, epi, grid, tiles_n, tiles, st);
+      else launch_pipe_form<TGOHIP_FORM_I4_SYM, 64>(g, epi, grid, tiles_n, tiles, st);
+      break;
+    case TGOHIP_FORM_I4_TGO:
+      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_TGO, 128>(g, epi, grid, tiles_n, tiles, st);
+      else launch_pipe_form<TGOHIP_FORM_I4_TGO, 64>(g, epi, grid, tiles_n, tiles, st);
+      break;
+    default:
+      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I8, 128>(g, epi, grid, tiles_n, tiles, st);
+      else launch_pipe_form<TGOHIP_FORM_I8, 64>(g, epi, grid, tiles_n, tiles, st);
+      break;
+  }
   if (defer) *defer = splits > 1 ? splits : 0;
   if (splits > 1 && !defer) launch_reduce(g, epi, splits, st);
   TGOHIP_HIP(hipGetLastError());
@@ -871,10 +960,10 @@ static int pipe_min_rows() {
   return v;
 }
 
-// The pipelined kernel's register ring fits the int4-sym pack; other forms and
-// f32 activations use gemm_kernel.
+// The pipelined kernel serves the int4 packs and int8 with f16 activations;
+// f16 weights and f32 activations use gemm_kernel.
 static bool use_pipe(const PackedWeight& w, bool x_f32, int M) {
-  return !x_f32 && w.form == TGOHIP_FORM_I4_SYM && M >= pipe_min_rows() && (w.K / 64) % 4 == 0 &&
+  return !x_f32 && w.form != TGOHIP_FORM_F16 && M >= pipe_min_rows() && (w.K / 64) % 4 == 0 &&
          (int64_t)M * w.K < ((int64_t)1 << 31);  // its activation offsets are 32-bit
 }
 
