@@ -154,16 +154,20 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
         ctx.weight_free(h)
 
 
-@pytest.mark.parametrize("M", [96, 131, 300, 1152])
+@pytest.mark.parametrize("M", [33, 47, 96, 131, 300, 1152])
 @pytest.mark.parametrize("KN", [(2048, 416), (512, 4096)])
-def test_large_m_tiles_ragged_edges(ctx, torch_gpu, M, KN):
-    """The f16-activation path at M >= 96 (128-row tiles, XCD-dealt, split-K when
-    the tiles alone do not fill the chip): partial row and column tiles and every
+@pytest.mark.parametrize("form", [3, 2, 1])
+def test_large_m_tiles_ragged_edges(ctx, torch_gpu, M, KN, form):
+    """The pipelined f16-activation path at M >= 33 (64- and 128-row tiles,
+    XCD-dealt, split-K when the tiles alone do not fill the chip; int8 and tgo's
+    int4 with their scales through LDS): partial row and column tiles and every
     column checked against the f64 product of the same f16 operands."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN
-    h = ctx.weight_synth(3, K, N, 17, M, 0.02)
+    if form == 2 and N % 128:
+        N = 512  # tgo's int4 groups run along N in 128s
+    h = ctx.weight_synth(form, K, N, 17, M, 0.02)
     try:
         wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
         ctx.dequant_f16(h, wf)

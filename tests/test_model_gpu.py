@@ -140,6 +140,36 @@ def test_mixed_step_matches_the_cpu_path(torch_gpu, form, precision):
         cpu.close()
 
 
+WIDE = dict(layers=1, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=1024,
+            eps=1e-6, theta=1e6, block=16, positions=512)
+
+
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+def test_small_batch_step_on_the_small_m_kernel(torch_gpu, form):
+    """Qwen3-8B-wide projections (K = 4096 and 12288) at 3 and 2 rows: the
+    small-M kernel runs the QKV (f32 out), O (residual add), gate/up (SwiGLU)
+    and LM-head projections, every form, against the CPU path."""
+    cfg = WIDE
+    ctx, cpu = make_pair(torch_gpu, cfg, form, 31 + form, 0)
+    try:
+        engines = [Engine(b, cfg["vocab"], cfg["heads"], cfg["kv_heads"], cfg["positions"],
+                          cfg["block"], 2) for b in (gpu_backend(ctx), cpu_backend(cpu))]
+        rng = np.random.default_rng(7 + form)
+        p0 = [int(t) for t in rng.integers(0, cfg["vocab"], 2)]
+        p1 = [int(t) for t in rng.integers(0, cfg["vocab"], 1)]
+        for e in engines:
+            e.admit(0, p0, 4)
+            e.admit(1, p1, 4)
+        outs = [e.step([(0, p0), (1, p1)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1], "prefill")
+        t0, t1 = argmax_first(outs[1][0]), argmax_first(outs[1][1])
+        outs = [e.step([(0, [t0]), (1, [t1])]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1], "decode")
+    finally:
+        ctx.close()
+        cpu.close()
+
+
 @pytest.mark.parametrize("form", [3, 0])
 def test_long_chunk_step_matches_the_cpu_path(torch_gpu, form):
     """A 150-token chunk beside two decodes: the projections run at M >= 96 (the
