@@ -44,6 +44,13 @@ SLOTS = 136             # 128 decoders + 2 prefilling + headroom
 CHUNK = 512
 DECODERS = 128
 PREFILLING = 2
+# BASELINE config 5 (bench.py --config c5, a second workload; the default is config 4)
+C5 = dict(layers=64, hidden=5120, heads=64, kv_heads=8, head_dim=128, ffn=25600, vocab=151936,
+          rms_eps=1e-6, rope_theta=1e6, block=16)
+C5_PREFIX = 2048        # tokens every sequence begins with (128 shared pages)
+C5_DECODERS = 256
+C5_CHUNK = 1024
+C5_POOL = 330_000       # positions (86 GB of f16 K+V at 64 layers)
 HBM_PEAK = 8000.0       # GB/s, MI355X published
 MFMA_F16_PEAK = 2500.0  # TFLOP/s dense f16, MI355X published
 
@@ -61,6 +68,13 @@ def parse():
                    help="0: f16 activations into the MFMA (default); 1: f32 activations (hi+lo)")
     p.add_argument("--form", type=int, default=3, help="weight form (3: int4 sym g32-K, 2: tgo int4)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--config", default="c4", choices=["c4", "c5"],
+                   help="c4 (default): the headline workload; c5: BASELINE config 5, Qwen3-32B "
+                        "int8 with a 2048-token prefix shared by 256 sequences (prefix-shared "
+                        "attention on)")
+    p.add_argument("--cascade", type=int, default=2,
+                   help="config 5: group decode rows whose page tables share a prefix when at "
+                        "least this many do (0: off, every sequence reads its own prefix)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="before the workload, run one plain f32 copy kernel (torch.neg) over this "
                         "many MiB: the known-size dispatch that scales the HBM byte counters")
@@ -144,6 +158,124 @@ class Workload:
         return out, prefill, decodes, tm
 
 
+class SharedPrefixWorkload(Workload):
+    """256 decoding sequences that all begin with the same
+    2048-token prefix (its 128 pages held once by the prefix pool) followed by a
+    unique suffix of U[32, 1024] tokens, plus one arriving request prefilling in
+    1024-token chunks at every step. An arrival's prompt is the same prefix plus
+    a unique tail of U[1, 4] whole chunks, so the pool shares its prefix and
+    each step carries exactly one 1024-token chunk. Output budgets and
+    completions as in config 4."""
+
+    def __init__(self, tgo, ctx, seed):
+        self.rng = np.random.default_rng(seed)
+        self.sched = tgo.Scheduler(ctx, C5_DECODERS + 8, chunk=C5_CHUNK, reserve=512,
+                                   max_rows=C5_CHUNK + C5_DECODERS)
+        self.target, self.made, self.decoding = {}, {}, set()
+        self.V = C5["vocab"]
+        self.prefix = [int(t) for t in self.rng.integers(0, self.V, C5_PREFIX)]
+        used = C5_PREFIX
+        for _ in range(C5_DECODERS):
+            n = int(self.rng.integers(32, 1025))
+            out = int(self.rng.integers(100, 301))
+            prompt = self.prefix + [int(t) for t in self.rng.integers(0, self.V, n)]
+            slot = self.sched.admit_prefilled(prompt, int(self.rng.integers(0, self.V)), reserve=out)
+            self.target[slot], self.made[slot] = out, int(self.rng.integers(0, out))
+            self.decoding.add(slot)
+            used += n + out
+        self.used_positions = used
+        self.contexts = [self.sched.length(s) for s in sorted(self.decoding)]
+        self.admit_arrivals()
+
+    def admit_arrivals(self):
+        while self.sched.prefilling() < 1:
+            tail = C5_CHUNK * int(self.rng.integers(1, 5))
+            out = int(self.rng.integers(100, 301))
+            prompt = self.prefix + [int(t) for t in self.rng.integers(0, self.V, tail)]
+            slot = self.sched.admit(prompt, reserve=out)
+            self.target[slot], self.made[slot] = out, 0
+
+
+def run_c5(args, tgo_amd):
+    """BASELINE config 5 through the same Scheduler, with prefix-shared attention."""
+    form = 1 if args.form == 3 else args.form  # config 5 is an int8 model
+    t_setup = time.perf_counter()
+    ctx = tgo_amd.Context(0)
+    ctx.set_precision(args.precision)
+    ctx.set_cascade(args.cascade)
+    ctx.config(C5["layers"], C5["hidden"], C5["heads"], C5["kv_heads"], C5["head_dim"],
+               C5["ffn"], C5["vocab"], C5["rms_eps"], C5["rope_theta"], C5["block"])
+    ctx.synth_weights(SEED, form, 0.02)
+    ctx.kv_alloc(C5_POOL)
+    wl = SharedPrefixWorkload(tgo_amd, ctx, SEED)
+    ctx.kv_synth(SEED, 1.0, min(C5_POOL, wl.used_positions + 32 * C5_CHUNK))
+    print("setup %.1f s: config 5 weights synthesized, %d decoders admitted on a %d-token "
+          "shared prefix (mean context %.0f)" % (time.perf_counter() - t_setup, C5_DECODERS,
+          C5_PREFIX, np.mean(wl.contexts)), file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        wl.step()
+    ctx.sync()
+    ctx.set_profile(True)
+    total_out = total_pf = total_dc = 0
+    dev_ms = 0.0
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        out, pf, dc, tm = wl.step()
+        total_out += out
+        total_pf += pf
+        total_dc += dc
+        dev_ms += tm.device_ms
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    attn_ms, attn_bytes, launches = ctx.profile_read()
+    ctx.set_profile(False)
+    ctx.close()
+    avg_attn_ms = attn_ms / max(launches, 1)
+    achieved = (attn_bytes / max(launches, 1)) / (avg_attn_ms * 1e-3) / 1e9
+    return {
+        "metric": "output tok/s, Qwen3-32B int8 prefix-shared batch, 1 MI355X; paged-attn HBM GB/s",
+        "value": round(total_out / elapsed, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * elapsed / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.precision == 0 else "f16x2 (f32 activations)",
+        "data": "synthetic (seeded random-init int8 weights, seeded token ids, synthetic KV for "
+                "the initial contexts)",
+        "config": {
+            "workload": "BASELINE config 5: Qwen3-32B-shaped int8 (64 layers, hidden 5120, 64 q / "
+                        "8 kv heads, MLP 25600), 256 decode sequences on one 2048-token shared "
+                        "prefix + unique suffixes U[32,1024], one 1024-token prefill chunk per "
+                        "step, page 16, f16 KV, greedy, prefix-shared attention " +
+                        ("on (groups of >= %d)" % args.cascade if args.cascade else "off"),
+            "weight_form": {2: "int4-tgo-g128-asym", 1: "int8", 0: "f16"}.get(form, str(form)),
+            "rows_per_step": round((total_pf + total_dc) / args.steps, 1),
+            "prefill_tokens_per_step": round(total_pf / args.steps, 1),
+            "decodes_per_step": round(total_dc / args.steps, 1),
+            "output_tokens": int(total_out),
+            "device_ms_per_step": round(dev_ms / args.steps, 3),
+        },
+        "roofline": {
+            "kernel": "attn_kernel + attn_combine_kernel (ragged paged attention, shared "
+                      "prefix read once per group)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": None,
+            "avg_launch_ms": round(avg_attn_ms, 4),
+            "algorithmic_bytes_per_launch": round(attn_bytes / max(launches, 1)),
+            "launches": launches,
+        },
+        "cpu_baseline": None,
+    }
+
+
 def recorded_traffic():
     """HBM bytes per attention launch measured with rocprofv3 --pmc on this workload
     (FETCH_SIZE + WRITE_SIZE, each scaled by a copy probe), as profiles/ records it."""
@@ -194,6 +326,9 @@ def main():
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
     import tgo_amd
+    if args.config == "c5":
+        print(json.dumps(run_c5(args, tgo_amd)), flush=True)
+        return
     t_setup = time.perf_counter()
     ctx = tgo_amd.Context(0)
     ctx.set_precision(args.precision)

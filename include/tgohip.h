@@ -272,7 +272,9 @@ int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
                       tgohip_timings* t);
 
 /* Admits a sequence whose prompt's KV is already resident (restored, or
- * synthetic in a benchmark): the slot starts decoding with token `feed`. */
+ * synthetic in a benchmark): the slot starts decoding with token `feed`. The
+ * prompt's whole blocks are published, as a prefill publishes them, so a later
+ * prompt that begins with the same tokens shares those pages. */
 int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, int reserve,
                                  int feed);
 int tgohip_sched_prefilling(tgohip_sched* s); /* live slots still mid-prefill */

@@ -1286,6 +1286,11 @@ int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, 
   sl.prefilled = n;
   sl.length = n;
   sl.feed = feed;
+  // The prompt's KV is in place: its whole blocks are published, as a
+  // prefill would have published them, so later prompts that begin alike
+  // share them (publishing may adopt an identical block already cached).
+  sl.lease->publish(n);
+  sl.pages = sl.lease->blocks;
   return slot;
 }
 
