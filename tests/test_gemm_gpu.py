@@ -154,14 +154,16 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
         ctx.weight_free(h)
 
 
-@pytest.mark.parametrize("M", [33, 47, 96, 131, 300, 1152])
-@pytest.mark.parametrize("KN", [(2048, 416), (512, 4096)])
+@pytest.mark.parametrize("M", [33, 47, 96, 131, 300, 1000, 1152])
+@pytest.mark.parametrize("KN", [(2048, 416), (512, 4096), (512, 3712)])
 @pytest.mark.parametrize("form", [3, 2, 1])
 def test_large_m_tiles_ragged_edges(ctx, torch_gpu, M, KN, form):
-    """The pipelined f16-activation path at M >= 33 (64- and 128-row tiles,
-    XCD-dealt, split-K when the tiles alone do not fill the chip; int8 and tgo's
-    int4 with their scales through LDS): partial row and column tiles and every
-    column checked against the f64 product of the same f16 operands."""
+    """The pipelined f16-activation path at M >= 33 (64- and 128-row tiles, 4
+    or 8 waves wide, XCD-dealt, split-K when the tiles alone do not fill the
+    chip; int8 and tgo's int4 with their scales through LDS): partial row and
+    column tiles and every column checked against the f64 product of the same
+    f16 operands. N = 4096 and 3712 (116 column blocks: the last 512-column
+    tile holds 4) run 128-row tiles 8 waves wide."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN

@@ -18,11 +18,12 @@
 // Dequantized value: round-to-nearest-even f16 of the exact (q - z) * s, which
 // is computed with one exact packed subtraction and one rounded packed multiply.
 //
-// Tiling: 256 threads = 4 waves side by side in N; a workgroup owns MW rows x
-// 256 columns; each wave MW x 64 (MW/32 x 2 MFMA blocks of 32x32). The
-// activation tile (MW x 64 f16) is staged in LDS, XOR-swizzled: double-buffered
-// through registers in gemm_kernel, a four-stage ring filled by LDS DMA in
-// gemm_pipe_kernel. An f32 activation is carried as f16 hi + lo (two MFMAs) so
+// Tiling: waves side by side in N, each MW x 64 (MW/32 x 2 MFMA blocks of
+// 32x32); a workgroup of 4 waves owns MW rows x 256 columns (gemm_pipe_kernel
+// also runs 8 waves over 512 columns, which halves the activation tile's
+// reads per column). The activation tile (MW x 64 f16) is staged in LDS,
+// XOR-swizzled: double-buffered through registers in gemm_kernel, a
+// four-stage ring filled by LDS DMA in gemm_pipe_kernel. An f32 activation is carried as f16 hi + lo (two MFMAs) so
 // the product keeps ~22 bits of the activation. Split-K over grid.z writes f32
 // partials that a reduction kernel (or the consumer) sums in split order
 // (deterministic).
@@ -418,10 +419,12 @@ __device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I8>& r, in
   return deq_i8((j & 1) ? q.z : q.x, (j & 1) ? q.w : q.y, s8);
 }
 
-template <int FORM, int EPI, int MW>
-__global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles_n, int tiles) {
+// NW waves (4 or 8) side by side in N: a workgroup owns MW rows x 64*NW columns.
+template <int FORM, int EPI, int MW, int NW>
+__global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs g, int tiles_n,
+                                                                       int tiles) {
   constexpr int MB = MW / 32;
-  constexpr int ACH = MW / 32;  // 1 KiB LDS-DMA chunks per wave per k-step
+  constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step
   // Four LDS stages, separate arrays so the compiler can tell a DMA into one
   // stage from reads of another.
   __shared__ __attribute__((aligned(16))) half_t As0[MW * 64];
@@ -429,9 +432,9 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   __shared__ __attribute__((aligned(16))) half_t As2[MW * 64];
   __shared__ __attribute__((aligned(16))) half_t As3[MW * 64];
   half_t* const As[4] = {As0, As1, As2, As3};
-  // Per-stage scales and zeros of the four waves' column blocks (int8, tgo int4).
+  // Per-stage scales and zeros of the waves' column blocks (int8, tgo int4).
   constexpr bool LS = pipe_lds_scales<FORM>();
-  constexpr int SZN = LS ? 4 * 256 : 8;
+  constexpr int SZN = LS ? NW * 256 : 8;
   __shared__ __attribute__((aligned(16))) half_t Sz0[SZN];
   __shared__ __attribute__((aligned(16))) half_t Sz1[SZN];
   __shared__ __attribute__((aligned(16))) half_t Sz2[SZN];
@@ -450,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   const int h = lane >> 5, c32 = lane & 31;
   const int NBT = g.N / 32;
-  const int nbw0 = tn * 8 + wave * 2;
+  const int nbw0 = tn * 2 * NW + wave * 2;
   const int m0 = tm * MW;
   const int KS = g.K / 64;
   const int ks0 = blockIdx.z * g.ksteps_per_split;
@@ -460,14 +463,14 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
   const int nbl[2] = {min(nbw0, NBT - 1), min(nbw0 + 1, NBT - 1)};
 
   // The A tile goes global -> LDS by DMA (global_load_lds_dwordx4): lane l of
-  // wave w's chunk i writes the 16-byte slot p = (4i + w)*64 + l, which holds
+  // wave w's chunk i writes the 16-byte slot p = (NW*i + w)*64 + l, which holds
   // (row p/8, k-chunk (p%8) ^ ((row/2)%8)) of the swizzled tile. Rows past M
   // load row M-1 (their results are not stored). Byte offsets fit 32 bits:
   // the host checks M*K.
   uint32_t doff[ACH];
 #pragma unroll
   for (int i = 0; i < ACH; i++) {
-    const int p = (4 * i + wave) * 64 + lane, row = p >> 3, kc = (p & 7) ^ ((row >> 1) & 7);
+    const int p = (NW * i + wave) * 64 + lane, row = p >> 3, kc = (p & 7) ^ ((row >> 1) & 7);
     doff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)(kc * 8)) * 2u;
   }
   const char* xa = (const char*)g.x;
@@ -483,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs g, int tiles
     _Pragma("unroll") for (int i = 0; i < ACH; i++)                                    \
         __builtin_amdgcn_global_load_lds(                                              \
             (const __attribute__((address_space(1))) void*)(xa + (size_t)(ks) * 128 + doff[i]), \
-            (__attribute__((address_space(3))) void*)(As[stage] + (4 * i + wave) * 512), 16, 0, 0); \
+            (__attribute__((address_space(3))) void*)(As[stage] + (NW * i + wave) * 512), 16, 0, 0); \
     if (LS && szlane)                                                                  \
       __builtin_amdgcn_global_load_lds(                                                \
           (const __attribute__((address_space(1))) void*)(szsrc + (size_t)(ks) * 128), \
@@ -992,8 +995,8 @@ static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st
 // Split-K factor for the pipelined kernel: none when the tiles fill at least
 // half the chip's slots (2 per CU); otherwise as many splits as fit in one
 // round of slots, keeping >= 8 k-steps per split.
-static int choose_pipe_splits(int tiles, int KS, int ncu) {
-  const int slots = 2 * ncu;
+// slots: workgroups the chip holds at once.
+static int choose_pipe_splits(int tiles, int KS, int slots) {
   if (tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
   int s = slots / tiles;              // one round of workgroups
   while (s > 1 && KS / s < 8) s--;
@@ -1006,41 +1009,57 @@ static int choose_pipe_splits(int tiles, int KS, int ncu) {
 // dequantization per MFMA) with split-K when they underfill the chip.
 // Measured on the C3/C4 shapes: 64-row tiles without split-K lose to 128-row
 // tiles with split-K at M = 1152, N = 4096.
-static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& tiles_n, int& tiles,
-                       int& splits) {
-  tiles_n = (w.N / 32 + 7) / 8;
+// 128-row tiles go 8 waves wide (512 columns, one workgroup per CU) when the
+// 512-column tiles deal evenly over the 8 XCDs: each activation tile read
+// from L2 then feeds twice the columns (gate/up and down at M = 1152 measured
+// 3-4% faster); otherwise 4 waves (256 columns, two workgroups per CU) keep
+// the XCDs balanced (QKV, N = 6144: 12 wide tiles would leave four XCDs
+// half idle, 45% slower).
+static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, int& tiles_n,
+                       int& tiles, int& splits) {
   mw = M <= 384 ? 64 : 128;
+  const int nb = w.N / 32;
+  nw = (mw == 128 && ((nb + 15) / 16) % 8 == 0) ? 8 : 4;
+  tiles_n = (nb + 2 * nw - 1) / (2 * nw);
   tiles = tiles_n * ((M + mw - 1) / mw);
-  splits = choose_pipe_splits(tiles, w.K / 64, ncu);
+  splits = choose_pipe_splits(tiles, w.K / 64, ncu * (8 / nw));
 }
 
 // Workspace bytes a call needs for split-K partials.
 size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   int s = choose_splits(M, w.N, w.K, MW, ncu);
-  int mw, tiles_n, tiles, ps;
-  pipe_shape(w, M, ncu, mw, tiles_n, tiles, ps);
+  int mw, nw, tiles_n, tiles, ps;
+  pipe_shape(w, M, ncu, mw, nw, tiles_n, tiles, ps);
   s = std::max(s, ps);
   return s > 1 ? (size_t)s * M * w.N * sizeof(float) : 0;
 }
 
-template <int FORM, int MW>
+template <int FORM, int MW, int NW>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
                              hipStream_t st) {
-  const dim3 blk(256);
+  const dim3 blk(64 * NW);
   switch (epi) {
-    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
-    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles); break;
   }
+}
+
+template <int FORM>
+static void launch_pipe_shape(const GemmArgs& g, int epi, dim3 grid, int mw, int nw, int tiles_n,
+                              int tiles, hipStream_t st) {
+  if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, st);
+  else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, st);
+  else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, st);
 }
 
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
                              float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
-  int mw, tiles_n, tiles, splits;
-  pipe_shape(w, M, ncu, mw, tiles_n, tiles, splits);
+  int mw, nw, tiles_n, tiles, splits;
+  pipe_shape(w, M, ncu, mw, nw, tiles_n, tiles, splits);
   GemmArgs g{};
   g.x = x;
   g.wp = w.wp;
@@ -1062,16 +1081,13 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
   const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
   switch (w.form) {
     case TGOHIP_FORM_I4_SYM:
-      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_SYM, 128>(g, epi, grid, tiles_n, tiles, st);
-      else launch_pipe_form<TGOHIP_FORM_I4_SYM, 64>(g, epi, grid, tiles_n, tiles, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, tiles_n, tiles, st);
       break;
     case TGOHIP_FORM_I4_TGO:
-      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I4_TGO, 128>(g, epi, grid, tiles_n, tiles, st);
-      else launch_pipe_form<TGOHIP_FORM_I4_TGO, 64>(g, epi, grid, tiles_n, tiles, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, tiles_n, tiles, st);
       break;
     default:
-      if (mw == 128) launch_pipe_form<TGOHIP_FORM_I8, 128>(g, epi, grid, tiles_n, tiles, st);
-      else launch_pipe_form<TGOHIP_FORM_I8, 64>(g, epi, grid, tiles_n, tiles, st);
+      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, tiles_n, tiles, st);
       break;
   }
   if (defer) *defer = splits > 1 ? splits : 0;
