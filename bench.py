@@ -14,7 +14,11 @@ sequence frees its slot and the next arrival is admitted when fewer than two
 requests are mid-prefill. The initial 128 decoders are admitted with their
 context already in the pool (synthetic KV), so step 1 is already steady state.
 
-A step is one Scheduler.Step: one batched forward pass over ~1152 rows.
+A step is one Scheduler.Step: one batched forward pass over ~1152 rows. By
+default the scheduler runs in overlap mode: the host schedules and submits
+step k+1 while the device runs step k (the decode rows take their tokens from
+the device argmax), which runs the same steps and produces the same tokens as
+the synchronous mode (--sync).
 value = output tokens (sampleable tokens produced) / wall time of the timed
 steps, inputs resident in HBM. The roofline object is the ragged paged
 attention kernel (the metric's "paged-attn HBM GB/s"): algorithmic bytes per
@@ -68,6 +72,10 @@ def parse():
                    help="0: f16 activations into the MFMA (default); 1: f32 activations (hi+lo)")
     p.add_argument("--form", type=int, default=3, help="weight form (3: int4 sym g32-K, 2: tgo int4)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--sync", action="store_true",
+                   help="synchronous steps (tgo's Batch.step: pack, submit, wait, read back); "
+                        "the default overlaps the host's scheduling of step k+1 with the "
+                        "device's step k (the same steps and tokens)")
     p.add_argument("--config", default="c4", choices=["c4", "c5"],
                    help="c4 (default): the headline workload; c5: BASELINE config 5, Qwen3-32B "
                         "int8 with a 2048-token prefix shared by 256 sequences (prefix-shared "
@@ -136,11 +144,16 @@ class Workload:
             slot = self.sched.admit(prompt, reserve=out)
             self.target[slot], self.made[slot] = out, 0
 
-    def step(self):
-        produced, prefill, decodes, tm = self.sched.step()
+    def decide(self, produced, tokens=None):
+        """The books after a step: produced is [(slot, done)]. Each request that started
+        decoding retires the decoder nearest its budget; arrivals refill the prefill
+        slots. tokens ({slot: token}, synchronous mode) are fed back; in overlap mode the
+        scheduler feeds them on the device. The decisions need no token values, so in
+        overlap mode they are taken before the step is read back, and the steps are those
+        of synchronous mode."""
         out = 0
         started = 0
-        for slot, tok, done in produced:
+        for slot, done in produced:
             if not done:
                 continue
             out += 1
@@ -148,14 +161,70 @@ class Workload:
             if slot not in self.decoding:
                 self.decoding.add(slot)
                 started += 1
-            self.sched.feed(slot, tok)
-        # each request that started decoding retires the decoder nearest its budget
+            if tokens is not None:
+                self.sched.feed(slot, tokens[slot])
         for _ in range(started):
             slot = max(self.decoding, key=lambda s: (self.made[s] / self.target[s], -s))
             self.decoding.discard(slot)
             self.sched.finish(slot)
         self.admit_arrivals()
+        return out
+
+    def step(self):
+        """One synchronous step: (output tokens, prefill tokens, decodes, timings)."""
+        produced, prefill, decodes, tm = self.sched.step()
+        out = self.decide([(s, d) for s, _, d in produced], {s: t for s, t, d in produced if d})
         return out, prefill, decodes, tm
+
+    def submit(self):
+        """Overlap mode: enqueue the next step and take its decisions at once."""
+        info, prefill, decodes = self.sched.submit()
+        out = self.decide(info)
+        return out, prefill, decodes
+
+
+def run_steps(wl, ctx, steps, warmup, sync):
+    """Warm-up steps, then exactly `steps` timed steps. Overlap mode keeps one step
+    in flight while the host schedules the next; the pipeline starts empty and is
+    drained inside the timed region, so the wall time covers exactly the timed
+    steps. -> (elapsed s, output tokens, prefill tokens, decodes, device ms)."""
+    if not sync:
+        wl.sched.set_overlap(True)
+
+    def run(n, timed):
+        tot = [0, 0, 0, 0.0]
+        if sync:
+            for i in range(n):
+                out, pf, dc, tm = wl.step()
+                tot[0] += out
+                tot[1] += pf
+                tot[2] += dc
+                tot[3] += tm.device_ms
+                if timed and (i + 1) % 50 == 0:
+                    print("step %d/%d" % (i + 1, n), file=sys.stderr, flush=True)
+            return tot
+        flight = [wl.submit()] if n else []
+        for i in range(n):
+            if i + 1 < n:
+                flight.append(wl.submit())
+            _, tm = wl.sched.collect()
+            out, pf, dc = flight.pop(0)
+            tot[0] += out
+            tot[1] += pf
+            tot[2] += dc
+            tot[3] += tm.device_ms
+            if timed and (i + 1) % 50 == 0:
+                print("step %d/%d" % (i + 1, n), file=sys.stderr, flush=True)
+        return tot
+
+    run(warmup, False)
+    ctx.sync()
+    ctx.set_profile(True)
+    t0 = time.perf_counter()
+    out, pf, dc, dev_ms = run(steps, True)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    return elapsed, out, pf, dc, dev_ms
 
 
 class SharedPrefixWorkload(Workload):
@@ -212,21 +281,8 @@ def run_c5(args, tgo_amd):
     print("setup %.1f s: config 5 weights synthesized, %d decoders admitted on a %d-token "
           "shared prefix (mean context %.0f)" % (time.perf_counter() - t_setup, C5_DECODERS,
           C5_PREFIX, np.mean(wl.contexts)), file=sys.stderr, flush=True)
-    for i in range(args.warmup):
-        wl.step()
-    ctx.sync()
-    ctx.set_profile(True)
-    total_out = total_pf = total_dc = 0
-    dev_ms = 0.0
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        out, pf, dc, tm = wl.step()
-        total_out += out
-        total_pf += pf
-        total_dc += dc
-        dev_ms += tm.device_ms
-    ctx.sync()
-    elapsed = time.perf_counter() - t0
+    elapsed, total_out, total_pf, total_dc, dev_ms = run_steps(wl, ctx, args.steps, args.warmup,
+                                                               args.sync)
     attn_ms, attn_bytes, launches = ctx.profile_read()
     ctx.set_profile(False)
     ctx.close()
@@ -258,6 +314,7 @@ def run_c5(args, tgo_amd):
             "decodes_per_step": round(total_dc / args.steps, 1),
             "output_tokens": int(total_out),
             "device_ms_per_step": round(dev_ms / args.steps, 3),
+            "host_overlap": not args.sync,
         },
         "roofline": {
             "kernel": "attn_kernel + attn_combine_kernel (ragged paged attention, shared "
@@ -343,24 +400,8 @@ def main():
           (setup_s, DECODERS, np.mean([x for x in wl.contexts if x > 0])), file=sys.stderr,
           flush=True)
 
-    for i in range(args.warmup):
-        wl.step()
-    ctx.sync()
-    ctx.set_profile(True)
-    total_out = total_pf = total_dc = 0
-    dev_ms = 0.0
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        out, pf, dc, tm = wl.step()
-        total_out += out
-        total_pf += pf
-        total_dc += dc
-        dev_ms += tm.device_ms
-        if (i + 1) % 50 == 0:
-            print("step %d/%d: %.1f ms/step so far" % (i + 1, args.steps,
-                  1e3 * (time.perf_counter() - t0) / (i + 1)), file=sys.stderr, flush=True)
-    ctx.sync()
-    elapsed = time.perf_counter() - t0
+    elapsed, total_out, total_pf, total_dc, dev_ms = run_steps(wl, ctx, args.steps, args.warmup,
+                                                               args.sync)
     attn_ms, attn_bytes, launches = ctx.profile_read()
     ctx.set_profile(False)
     last_st, last_pages, maxp = wl.sched.last_step()
@@ -395,6 +436,7 @@ def main():
             "decodes_per_step": round(total_dc / args.steps, 1),
             "output_tokens": int(total_out),
             "device_ms_per_step": round(dev_ms / args.steps, 3),
+            "host_overlap": not args.sync,
         },
         "roofline": {
             "kernel": "attn_kernel + attn_combine_kernel (ragged paged attention)",

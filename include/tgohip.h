@@ -138,9 +138,9 @@ typedef struct {
   int32_t batch;             /* B members */
   int32_t max_pages;         /* page-table width */
   const uint32_t* ids;       /* host [rows]        model.BatchStep.IDs */
-  const uint32_t* posq;      /* host [rows*H]      .PosQ */
-  const uint32_t* posk;      /* host [rows*H_kv]   .PosK */
-  const uint32_t* slots;     /* host [rows]        .Slots */
+  const uint32_t* posq;      /* host [rows*H]      .PosQ  (or NULL, see below) */
+  const uint32_t* posk;      /* host [rows*H_kv]   .PosK  (or NULL) */
+  const uint32_t* slots;     /* host [rows]        .Slots (or NULL) */
   const uint32_t* lengths;   /* host [B]           .Lengths */
   const uint32_t* extents;   /* host [B]           .Extents */
   const uint32_t* last;      /* host [B]           .Last */
@@ -156,7 +156,14 @@ typedef struct {
 /* Runs the whole forward pass for one step. logits_out: host [B,V] f32 or
  * NULL; rows of members with extent 0 are zero. argmax_out: host [B] int32 or
  * NULL: the greedy token per member (sample/stages.go:196-206, first strict
- * maximum; -1 for extent 0). timings may be NULL. */
+ * maximum; -1 for extent 0). timings may be NULL.
+ * posq, posk and slots may all be NULL (no counterpart in tgo, whose
+ * NewBatchStep packs them, batch.go:310-340): the device derives them from the
+ * members, the values NewBatchStep would pack. Row t belongs to the last member
+ * b with cu_b <= t (cu: prefix sums of extents) and sits at position
+ * p = lengths[b] - extents[b] + (t - cu_b), slot pages[b][p / block] * block +
+ * p % block; rows past sum(extents) repeat the last member's last position
+ * with slot = capacity. Only ids and the per-member ports then cross PCIe. */
 int tgohip_step(tgohip_ctx* ctx, const tgohip_batch_step* step, float* logits_out,
                 int32_t* argmax_out, tgohip_timings* timings);
 
@@ -285,6 +292,32 @@ int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32
                            uint32_t* ids, uint32_t* posq, uint32_t* posk, uint32_t* slots,
                            uint32_t* lengths, uint32_t* extents, uint32_t* last,
                            uint32_t* pages);
+
+/* Overlap mode (no counterpart in tgo, whose Batch.step packs, submits, waits
+ * and reads back under the model's lock, batch.go:381-437; it is the host /
+ * device overlap the path's next steps ask for). tgohip_sched_submit enqueues
+ * the next step and returns without waiting; tgohip_sched_collect waits for
+ * the oldest step in flight, commits it and reports its tokens. At most two
+ * steps are in flight, so the host schedules step k+1 while the device runs
+ * step k. A decode row's token is the previous step's argmax, read on the
+ * device, and posq/posk/slots are derived on the device (tgohip_step with
+ * NULL ports). The scheduler feeds every generated token itself:
+ * tgohip_sched_feed refuses a slot it feeds. tgohip_sched_finish of a slot
+ * with rows in flight takes effect for later submits at once and releases
+ * its pages when those rows land. tgohip_sched_prefilling counts as if the
+ * steps in flight had landed. Steps, and the tokens they produce, are those of
+ * tgohip_sched_step when the caller admits and finishes the same sequences
+ * before each submit as it would before each step. The context's argmax
+ * buffer belongs to the scheduler between submits. */
+int tgohip_sched_set_overlap(tgohip_sched* s, int on);
+/* out arrays sized n: slot and done (0/1) per producing slot, in the order
+ * collect reports them. Returns the count (0: nothing to step). */
+int tgohip_sched_submit(tgohip_sched* s, int32_t* out_slot, int32_t* out_done,
+                        int32_t* prefill_tokens, int32_t* decodes);
+/* out arrays sized n: slot, token (greedy), done, as tgohip_sched_step
+ * reports them. Returns the count (0: nothing in flight). */
+int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
+                         int32_t* out_done, tgohip_timings* t);
 
 /* ---- measurement ------------------------------------------------------- */
 /* Brackets every attention launch of tgohip_step with HIP events on the

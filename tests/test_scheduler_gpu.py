@@ -1,0 +1,216 @@
+"""The library's Scheduler on the GPU: steps with posq/posk/slots derived on
+the device, and overlap mode (submit / collect) against the synchronous step.
+
+* A step whose posq, posk and slots are left to the device gives the same
+  logits, to the bit, as the same step with NewBatchStep's packed ports
+  (model.NewBatchStep, batch.go:310-340, restated in oracle/host.py), padding
+  rows included.
+* Overlap mode runs the steps the synchronous scheduler runs when the caller
+  admits and retires the same sequences before each submit as before each
+  step. Each sequence's greedy tokens are then identical: a row's result does
+  not depend on the rows beside it at a given step size, and the attention of
+  a sequence is the same mixed or apart (ragged_test.go:295).
+"""
+import numpy as np
+import pytest
+
+import tgo_amd
+from oracle import host
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1024,
+           eps=1e-6, theta=1e6, block=4, positions=1024)
+
+
+def new_ctx(torch, form=3, seed=21):
+    c = CFG
+    ctx = tgo_amd.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    ctx.config(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"],
+               c["vocab"], c["eps"], c["theta"], c["block"])
+    ctx.synth_weights(seed, form, 0.02)
+    ctx.kv_alloc(c["positions"])
+    return ctx
+
+
+def packed_step(rng, rows_pad):
+    """Three members (a prefill chunk, a decode, an idle one) packed by NewBatchStep, plus
+    rows_pad padding rows."""
+    c = CFG
+    pool = host.Pool(c["block"], c["positions"] // c["block"])
+    members = []
+    for n_prompt, n_new in ((13, 13), (0, 0), (9, 1)):
+        if n_prompt == 0:
+            members.append(host.Member([], 0, []))
+            continue
+        toks = [int(t) for t in rng.integers(0, c["vocab"], n_prompt)]
+        lease = pool.acquire(toks, reserve=4)  # blocks for the prompt and 4 more
+        first = n_prompt - n_new
+        members.append(host.Member(toks[first:], first, list(lease.blocks)))
+    rows = sum(len(m.tokens) for m in members) + rows_pad
+    st = host.new_batch_step(c["vocab"], c["heads"], c["kv_heads"], rows, members, c["block"],
+                             c["positions"])
+    max_pages = c["positions"] // c["block"]
+    table = host.page_table([m.pages for m in members], max_pages)
+    return st, table, max_pages
+
+
+@pytest.mark.parametrize("rows_pad", [0, 3])
+def test_derived_ports_equal_the_packed_ports(torch_gpu, rows_pad):
+    torch = torch_gpu
+    st, table, max_pages = packed_step(np.random.default_rng(5), rows_pad)
+    a, b = new_ctx(torch), new_ctx(torch)
+    la, aa, _ = a.step(st, table, max_pages)
+    derived = dict(st, posq=None, posk=None, slots=None)
+    lb, ab, _ = b.step(derived, table, max_pages)
+    assert np.isfinite(la).all()
+    assert np.array_equal(la, lb)
+    assert np.array_equal(aa, ab)
+    # the KV pools the two steps wrote, every layer (padding rows write nothing)
+    torch.cuda.synchronize()
+    pools = [pool_copy(x) for x in (a, b)]
+    assert np.array_equal(pools[0], pools[1])
+    assert np.count_nonzero(pools[0]) > 0
+    a.close()
+    b.close()
+
+
+def pool_copy(ctx):
+    """Both KV pools of every layer, copied to the host as f16 bits."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    k, v, positions = ctx.kv_pointers()
+    n = CFG["layers"] * positions * CFG["kv_heads"] * CFG["head_dim"]
+    out = np.empty((2, n), np.uint16)
+    for i, src in enumerate((k, v)):
+        assert hip.hipMemcpy(out[i].ctypes.data, src, n * 2, 2) == 0  # device to host
+    return out
+
+
+class Driver:
+    """Arrivals and retirements around a scheduler: at most `target` live sequences, each
+    retired after `budget` generated tokens. The decisions after a step depend only on
+    which slots produced a token, so they can be taken before the step is read back."""
+
+    def __init__(self, sched, seed, target, count):
+        rng = np.random.default_rng(seed)
+        V = CFG["vocab"]
+        self.queue = [([int(t) for t in rng.integers(0, V, int(rng.integers(3, 21)))],
+                       int(rng.integers(2, 9))) for _ in range(count)]
+        self.sched, self.target = sched, target
+        self.seq_of, self.made, self.budget = {}, {}, {}
+        self.next_seq = 0
+        self.admit()
+
+    def admit(self):
+        while self.sched.live() < self.target and self.queue:
+            prompt, budget = self.queue.pop(0)
+            slot = self.sched.admit(prompt, reserve=budget + 1)
+            self.seq_of[slot] = self.next_seq
+            self.made[slot], self.budget[slot] = 0, budget
+            self.next_seq += 1
+
+    def decide(self, produced, tokens=None):
+        """produced: [(slot, done)]; tokens (sync mode): {slot: token} to feed."""
+        for slot, done in produced:
+            if not done:
+                continue
+            self.made[slot] += 1
+            if self.made[slot] >= self.budget[slot]:
+                self.sched.finish(slot)
+                del self.seq_of[slot]
+            elif tokens is not None:
+                self.sched.feed(slot, tokens[slot])
+        self.admit()
+
+
+def run_sync(sched, steps):
+    d = Driver(sched, 3, 5, 30)
+    streams, sizes = {}, []
+    for _ in range(steps):
+        produced, pf, dc, _ = sched.step()
+        sizes.append((pf, dc))
+        toks = {}
+        for slot, tok, done in produced:
+            if done:
+                streams.setdefault(d.seq_of[slot], []).append(tok)
+                toks[slot] = tok
+        d.decide([(s, dn) for s, _, dn in produced], toks)
+    return streams, sizes
+
+
+def run_overlap(sched, steps):
+    sched.set_overlap(True)
+    d = Driver(sched, 3, 5, 30)
+    streams, sizes = {}, []
+    labels = []  # per step in flight: {slot: sequence} when it was submitted
+    info, pf, dc = sched.submit()
+    sizes.append((pf, dc))
+    labels.append(dict(d.seq_of))
+    d.decide(info)
+    for k in range(steps):
+        if k + 1 < steps:
+            nxt, pf, dc = sched.submit()
+            sizes.append((pf, dc))
+            labels.append(dict(d.seq_of))
+        produced, _ = sched.collect()
+        seqs = labels.pop(0)
+        for slot, tok, done in produced:
+            if done:
+                streams.setdefault(seqs[slot], []).append(tok)
+        if k + 1 < steps:
+            d.decide(nxt)
+    assert sched.collect()[0] == []  # nothing left in flight
+    return streams, sizes
+
+
+def test_overlap_mode_runs_the_synchronous_steps(torch_gpu):
+    torch = torch_gpu
+    steps = 40
+    a, b = new_ctx(torch), new_ctx(torch)
+    sa = tgo_amd.Scheduler(a, 8, chunk=8, reserve=4, max_rows=64)
+    sb = tgo_amd.Scheduler(b, 8, chunk=8, reserve=4, max_rows=64)
+    sync_streams, sync_sizes = run_sync(sa, steps)
+    ov_streams, ov_sizes = run_overlap(sb, steps)
+    assert sync_sizes == ov_sizes
+    assert len(sync_streams) >= 10
+    assert sync_streams == ov_streams
+    sa.close()
+    sb.close()
+    a.close()
+    b.close()
+
+
+def test_overlap_refusals(torch_gpu):
+    torch = torch_gpu
+    ctx = new_ctx(torch)
+    s = tgo_amd.Scheduler(ctx, 4, chunk=8, reserve=4, max_rows=64)
+    with pytest.raises(tgo_amd.TgoError, match="overlap mode"):
+        s.submit()
+    slot = s.admit([1, 2, 3], reserve=8)
+    s.set_overlap(True)
+    with pytest.raises(tgo_amd.TgoError, match="tgohip_sched_submit"):
+        s.step()
+    info, _, _ = s.submit()
+    assert info == [(slot, True)]
+    with pytest.raises(tgo_amd.TgoError, match="feeds each generated token itself"):
+        s.feed(slot, 7)
+    with pytest.raises(tgo_amd.TgoError, match="in flight"):
+        s.set_overlap(False)
+    s.submit()
+    with pytest.raises(tgo_amd.TgoError, match="two steps are in flight"):
+        s.submit()
+    # a slot finished with rows in flight is not reused until they land
+    s.finish(slot)
+    with pytest.raises(tgo_amd.TgoError):
+        for _ in range(4):
+            s.admit([5, 6], reserve=2)
+    out1, _ = s.collect()
+    out2, _ = s.collect()
+    assert [o[0] for o in out1] == [slot] and [o[0] for o in out2] == [slot]
+    assert out2[0][1] >= 0
+    s.set_overlap(False)
+    s.close()
+    ctx.close()

@@ -112,6 +112,9 @@ def lib():
         "tgohip_sched_prefilling": (I, [P]),
         "tgohip_sched_live": (I, [P]),
         "tgohip_sched_last_step": (I, [P, P, P, P, P, P, P, P, P, P, P, P]),
+        "tgohip_sched_set_overlap": (I, [P, I]),
+        "tgohip_sched_submit": (I, [P, P, P, P, P]),
+        "tgohip_sched_collect": (I, [P, P, P, P, ctypes.POINTER(Timings)]),
         "tgohip_set_profile": (I, [P, I]),
         "tgohip_profile_read": (I, [P, P, P, P]),
         "tgohip_kv_synth": (I, [P, U64, D, I]),
@@ -492,11 +495,13 @@ class Context:
         return k.value, v.value, n.value
 
     def step(self, st, pages, max_pages, want_logits=True, want_argmax=True):
-        """Batch.step's device half (batch.go:384-437). st: ports (dict of arrays)."""
-        keep = {k: u32(v) for k, v in st.items()}
+        """Batch.step's device half (batch.go:384-437). st: ports (dict of arrays).
+        posq, posk and slots may be None (absent) together: the device derives them."""
+        keep = {k: (u32(v) if v is not None else None) for k, v in st.items()}
         pg = u32(pages)
         B = len(keep["lengths"])
-        c = BatchStepC(len(keep["ids"]), B, max_pages, *(ptr(keep[n]).value for n in (
+        addr = lambda a: None if a is None else ptr(a).value
+        c = BatchStepC(len(keep["ids"]), B, max_pages, *(addr(keep.get(n)) for n in (
             "ids", "posq", "posk", "slots", "lengths", "extents", "last")), ptr(pg).value)
         logits = np.zeros((B, self.cfg["vocab"]), np.float32) if want_logits else None
         am = np.zeros(B, np.int32) if want_argmax else None
@@ -609,6 +614,26 @@ class Scheduler:
         n = check(lib().tgohip_sched_step(self.h, ptr(s), ptr(t), ptr(d), ctypes.byref(pf),
                                           ctypes.byref(dc), ctypes.byref(tm)))
         return [(int(s[i]), int(t[i]), bool(d[i])) for i in range(n)], pf.value, dc.value, tm
+
+    # ---- overlap mode: submit the next step before the last is read back ----
+    def set_overlap(self, on):
+        check(lib().tgohip_sched_set_overlap(self.h, 1 if on else 0))
+
+    def submit(self):
+        """Enqueues the next step. -> ([(slot, done)], prefill_tokens, decodes); an empty
+        list when there is nothing to step."""
+        s, d = np.zeros(self.n, np.int32), np.zeros(self.n, np.int32)
+        pf, dc = ctypes.c_int32(), ctypes.c_int32()
+        n = check(lib().tgohip_sched_submit(self.h, ptr(s), ptr(d), ctypes.byref(pf),
+                                            ctypes.byref(dc)))
+        return [(int(s[i]), bool(d[i])) for i in range(n)], pf.value, dc.value
+
+    def collect(self):
+        """Waits for the oldest step in flight. -> ([(slot, greedy token, done)], timings)."""
+        s, t, d = (np.zeros(self.n, np.int32) for _ in range(3))
+        tm = Timings()
+        n = check(lib().tgohip_sched_collect(self.h, ptr(s), ptr(t), ptr(d), ctypes.byref(tm)))
+        return [(int(s[i]), int(t[i]), bool(d[i])) for i in range(n)], tm
 
     def close(self):
         if self.h:

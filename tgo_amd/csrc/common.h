@@ -131,9 +131,18 @@ struct QKRopeArgs {
   size_t plane;           // elements per partial plane
   const float* qnorm;     // [128]
   const float* knorm;     // [128]
-  const uint32_t* posq;   // [T*H]
+  const uint32_t* posq;   // [T*H], or null: derived from the members below
   const uint32_t* posk;   // [T*Hkv]
   const uint32_t* slots;  // [T]
+  // Members, for posq/posk/slots derived on the device: row t belongs to the
+  // last member b with cu[b] <= t, at position lengths[b] - extents[b] +
+  // (t - cu[b]), slot pages[b][p / block] * block + p % block. Rows past
+  // `total` repeat member `pad`'s last position with slot = capacity.
+  const int32_t* cu;
+  const uint32_t* lengths;
+  const uint32_t* extents;
+  const uint32_t* pages;
+  int B, max_pages, block, total, pad;
   const double* inv_freq; // [64]: base^(-2i/128), computed once on the host in double
   float* q;               // [T, H, 128]
   half_t* kc;             // layer view [C, Hkv, 128]
@@ -141,14 +150,17 @@ struct QKRopeArgs {
   int H, Hkv, capacity;
   float eps;
 };
+// ids[t] with bit 31 set names a member b = ids[t] & 0x7fffffff whose token is
+// feed[b] (the previous step's argmax, left on the device).
 void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
-                  int d, float* h, hipStream_t st);
+                  int d, float* h, hipStream_t st, const int32_t* feed = nullptr);
 void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
                     float eps, void* out, int out_f16, hipStream_t st, const float* part = nullptr,
                     int nsplit = 0, size_t plane = 0);
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st);
+// keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1).
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st);
+                   hipStream_t st, int keep_idle = 0);
 void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st);
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st);

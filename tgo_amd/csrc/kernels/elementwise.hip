@@ -30,11 +30,14 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // h[t, :] = table[ids[t], :] (f16) or q * scale (int8, one scale per 32
-// flattened elements).
+// flattened elements). An id with bit 31 set is a member index whose token
+// is feed[member].
 __global__ void embed_kernel(const uint32_t* ids, const void* table, const uint16_t* scales,
-                             int form, int d, float* h) {
+                             int form, int d, float* h, const int32_t* feed) {
   const int t = blockIdx.x;
-  const size_t base = (size_t)ids[t] * d;
+  const uint32_t id = ids[t];
+  const uint32_t tok = (id >> 31) ? (uint32_t)feed[id & 0x7fffffffu] : id;
+  const size_t base = (size_t)tok * d;
   for (int i = threadIdx.x; i < d; i += blockDim.x) {
     float v;
     if (form == TGOHIP_FORM_F16) {
@@ -105,7 +108,37 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
     }
     return acc;
   };
-  const uint32_t slot = a.slots[t];
+  uint32_t slot;
+  int dpos = 0;  // the row's position when derived
+  if (a.slots) {
+    slot = a.slots[t];
+  } else {
+    __shared__ uint32_t sh[2];
+    if (threadIdx.x == 0) {
+      int b, p;
+      uint32_t sl;
+      if (t < a.total) {
+        int lo = 0, hi = a.B - 1;  // the last member with cu[b] <= t
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (a.cu[mid] <= t) lo = mid;
+          else hi = mid - 1;
+        }
+        b = lo;
+        p = (int)a.lengths[b] - (int)a.extents[b] + (t - a.cu[b]);
+        sl = a.pages[(size_t)b * a.max_pages + p / a.block] * (uint32_t)a.block + (uint32_t)(p % a.block);
+      } else {
+        b = a.pad;
+        p = (int)a.lengths[b] - 1;
+        sl = (uint32_t)a.capacity;
+      }
+      sh[0] = (uint32_t)p;
+      sh[1] = sl;
+    }
+    __syncthreads();
+    dpos = (int)sh[0];
+    slot = sh[1];
+  }
   const bool write = slot < (uint32_t)a.capacity;
   int cpos = -1;
   float c = 1.f, s = 0.f;
@@ -126,7 +159,9 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
     const float ss = wave_sum(v.x * v.x + v.y * v.y);
     const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
     const float x0 = v.x * sc * gain[2 * lane], x1 = v.y * sc * gain[2 * lane + 1];
-    const int pos = isq ? (int)a.posq[(size_t)t * a.H + hh] : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
+    const int pos = !a.posq ? dpos
+                    : isq   ? (int)a.posq[(size_t)t * a.H + hh]
+                            : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
     if (pos != cpos) {
       const double ang = (double)pos * inv;
       c = (float)cos(ang);
@@ -151,7 +186,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
 // 16-byte chunks in increasing index order, then the block reduces (larger
 // value, or equal value at a smaller index).
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V,
-                                                      const uint32_t* extents, int32_t* out) {
+                                                      const uint32_t* extents, int32_t* out,
+                                                      int keep_idle) {
   __shared__ float sv[16];
   __shared__ int si[16];
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -201,7 +237,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V
     const float x0 = row[0];
     int r = bi;
     if (x0 != x0 || bi == 0x7fffffff || !(best > x0)) r = 0;
-    out[b] = extents[b] == 0 ? -1 : r;
+    if (extents[b] != 0) out[b] = r;
+    else if (!keep_idle) out[b] = -1;
   }
 }
 
@@ -312,8 +349,8 @@ __global__ void zero_u32_kernel(uint32_t* p, size_t n) {
 static inline dim3 grid1(size_t n, int b = 256) { return dim3((unsigned)((n + b - 1) / b)); }
 
 void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
-                  int d, float* h, hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, st, ids, table, scales, form, d, h);
+                  int d, float* h, hipStream_t st, const int32_t* feed) {
+  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, st, ids, table, scales, form, d, h, feed);
 }
 void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
                     float eps, void* out, int out_f16, hipStream_t st, const float* part,
@@ -325,8 +362,8 @@ void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);
 }
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out);
+                   hipStream_t st, int keep_idle) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out, keep_idle);
 }
 void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st) {
   hipLaunchKernelGGL(zero_idle_rows_kernel, dim3(B), dim3(256), 0, st, logits, V, extents);

@@ -8,6 +8,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <memory>
 #include <string>
@@ -33,6 +34,9 @@ struct DevBuf {
   size_t bytes = 0;
   int ensure(size_t n) {
     if (n <= bytes) return 0;
+    // a step still in flight may read the old buffer (the scheduler's
+    // overlap mode): let the device drain before it goes
+    if (p) (void)hipDeviceSynchronize();
     if (p) (void)hipFree(p);
     p = nullptr;
     bytes = 0;
@@ -700,10 +704,22 @@ int tgohip_kv_pointers(tgohip_ctx* c, void** k, void** v, int* positions) {
 }
 
 // ---- the batched step ------------------------------------------------------
-int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, int32_t* argmax_out,
-                tgohip_timings* tm) {
-  using clk = std::chrono::steady_clock;
-  const auto t_start = clk::now();
+}  // extern "C"
+
+namespace {
+
+// One step's device work, enqueued on c->stream without waiting: the ports
+// staged and uploaded, every kernel launched, ev_begin / ev_end recorded
+// around them. The argmax of every member is left in c->argmax.
+struct StepLaunch {
+  const int32_t* feed = nullptr;  // ids with bit 31 set take feed[member] (device)
+  int keep_idle = 0;              // argmax leaves the entries of idle members as they are
+  hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+  int prof_set = 0;               // which set of attention profile events
+  double attn_bytes = 0;          // out: algorithmic bytes of one attention launch
+};
+
+int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   if (!c->configured) return fail(TGOHIP_ESTATE, "step: configure the context first");
   if (!c->kc) return fail(TGOHIP_ESTATE, "step: a batched step needs a shared block pool (kv_alloc)");
   const tgohip_model_cfg& m = c->cfg;
@@ -717,10 +733,22 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   }
   const int T = s->rows, B = s->batch;
   if (T <= 0 || B <= 0) return fail(TGOHIP_EINVAL, "step: rows and batch are positive");
-  for (int t = 0; t < T; t++)
+  for (int t = 0; t < T; t++) {
+    if (o.feed && (s->ids[t] >> 31)) {
+      if ((s->ids[t] & 0x7fffffffu) >= (uint32_t)B)
+        return fail(TGOHIP_EINVAL, "step: row " + std::to_string(t) + " takes the token of member " +
+                                       std::to_string(s->ids[t] & 0x7fffffffu) + " of " +
+                                       std::to_string(B));
+      continue;
+    }
     if (s->ids[t] >= (uint32_t)m.vocab)
       return fail(TGOHIP_EINVAL, "step: row " + std::to_string(t) + " token id " +
                                      std::to_string(s->ids[t]) + " is outside the vocabulary");
+  }
+  const bool derived = !s->posq;
+  if (derived != !s->posk || derived != !s->slots)
+    return fail(TGOHIP_EINVAL, "step: posq, posk and slots are given together, or all three are "
+                               "null and derived on the device from lengths, extents and pages");
   for (int b = 0; b < B; b++) {
     if (s->extents[b] > 0 && s->last[b] >= (uint32_t)T)
       return fail(TGOHIP_EINVAL, "step: member " + std::to_string(b) + " reads logits from row " +
@@ -730,15 +758,21 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   int rc = attn_build_plan(T, B, s->lengths, s->extents, s->pages, s->max_pages, m.block,
                            c->kv_positions, m.heads, m.kv_heads, plan, c->cascade);
   if (rc) return rc;
+  int pad = -1;
+  for (int b = 0; b < B; b++)
+    if (s->extents[b] > 0) pad = b;
+  if (derived && pad < 0)
+    return fail(TGOHIP_EINVAL, "step: every member contributes nothing; there are no positions "
+                               "to derive");
   if ((rc = ensure_activations(c, T, B))) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
 
   // One staged upload of every port (batch.go:385-405).
   Stager sg;
   const size_t o_ids = sg.add(s->ids, (size_t)T * 4);
-  const size_t o_posq = sg.add(s->posq, (size_t)T * m.heads * 4);
-  const size_t o_posk = sg.add(s->posk, (size_t)T * m.kv_heads * 4);
-  const size_t o_slots = sg.add(s->slots, (size_t)T * 4);
+  const size_t o_posq = derived ? 0 : sg.add(s->posq, (size_t)T * m.heads * 4);
+  const size_t o_posk = derived ? 0 : sg.add(s->posk, (size_t)T * m.kv_heads * 4);
+  const size_t o_slots = derived ? 0 : sg.add(s->slots, (size_t)T * 4);
   const size_t o_len = sg.add(s->lengths, (size_t)B * 4);
   const size_t o_ext = sg.add(s->extents, (size_t)B * 4);
   const size_t o_last = sg.add(s->last, (size_t)B * 4);
@@ -749,7 +783,7 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   const size_t o_seql = sg.add(plan.seqlist.data(), plan.seqlist.size() * sizeof(int32_t));
   if ((rc = sg.upload(c))) return rc;
   const hipStream_t st = c->stream;
-  TGOHIP_HIP(hipEventRecord(c->ev0, st));
+  TGOHIP_HIP(hipEventRecord(o.ev_begin, st));
 
   const uint32_t* d_ids = sg.dev<uint32_t>(c, o_ids);
   const uint32_t* d_ext = sg.dev<uint32_t>(c, o_ext);
@@ -767,19 +801,21 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
 
   // Algorithmic bytes of one attention launch: every cached position a
   // claimed row reads, once (K and V, all kv heads), plus q read and out written.
-  double attn_bytes = 0;
+  o.attn_bytes = 0;
+  hipEvent_t* pev = nullptr;
   if (c->profile) {
     for (int b = 0; b < B; b++)
-      if (s->extents[b] > 0) attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
-    attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (4 + (f32act ? 4 : 2));
-    attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
-    while ((int)c->prof_ev.size() < 2 * m.layers) {
+      if (s->extents[b] > 0) o.attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
+    o.attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (4 + (f32act ? 4 : 2));
+    o.attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
+    while ((int)c->prof_ev.size() < 4 * m.layers) {
       hipEvent_t e;
       TGOHIP_HIP(hipEventCreate(&e));
       c->prof_ev.push_back(e);
     }
+    pev = c->prof_ev.data() + (size_t)o.prof_set * 2 * m.layers;
   }
-  launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st);
+  launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
   // A split-K projection's partial planes are summed by the kernel that reads
   // its output next (in split order, so the result is the reduction's):
   // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
@@ -795,15 +831,18 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
       return rc;
     QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
                   (size_t)T * (m.heads + 2 * m.kv_heads) * kHeadDim, L.g_q, L.g_k,
-                  sg.dev<uint32_t>(c, o_posq), sg.dev<uint32_t>(c, o_posk),
-                  sg.dev<uint32_t>(c, o_slots), c->inv_freq, (float*)c->q.p, c->kc + l * layer_kv,
+                  derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
+                  derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
+                  derived ? nullptr : sg.dev<uint32_t>(c, o_slots),
+                  dp.cu, dp.lengths, d_ext, dp.pages, B, s->max_pages, m.block, plan.claimed, pad,
+                  c->inv_freq, (float*)c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps};
     launch_qk_rope_kv(qa, T, st);
-    if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l], st));
+    if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l], st));
     if ((rc = attn_enqueue(plan, dp, c->q.p, 0, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
-    if (c->profile) TGOHIP_HIP(hipEventRecord(c->prof_ev[2 * l + 1], st));
+    if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l + 1], st));
     if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
@@ -820,25 +859,48 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
   launch_zero_idle((float*)c->logits.p, B, m.vocab, d_ext, st);
-  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st);
-  TGOHIP_HIP(hipEventRecord(c->ev1, st));
+  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st, o.keep_idle);
+  TGOHIP_HIP(hipEventRecord(o.ev_end, st));
   TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
+// Adds one landed step's attention launches to the profile totals.
+int profile_collect(tgohip_ctx* c, int prof_set, double attn_bytes) {
+  if (!c->profile || c->prof_ev.size() < (size_t)4 * c->cfg.layers) return 0;
+  const hipEvent_t* pev = c->prof_ev.data() + (size_t)prof_set * 2 * c->cfg.layers;
+  for (int l = 0; l < c->cfg.layers; l++) {
+    float ms = 0;
+    TGOHIP_HIP(hipEventElapsedTime(&ms, pev[2 * l], pev[2 * l + 1]));
+    c->prof_attn_ms += ms;
+  }
+  c->prof_attn_launches += c->cfg.layers;
+  c->prof_attn_bytes += attn_bytes * c->cfg.layers;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, int32_t* argmax_out,
+                tgohip_timings* tm) {
+  using clk = std::chrono::steady_clock;
+  const auto t_start = clk::now();
+  StepLaunch o;
+  o.ev_begin = c->ev0;
+  o.ev_end = c->ev1;
+  int rc = step_launch(c, s, o);
+  if (rc) return rc;
   const auto t_sub = clk::now();
   TGOHIP_HIP(hipEventSynchronize(c->ev1));
   const auto t_dev = clk::now();
+  const tgohip_model_cfg& m = c->cfg;
   if (logits_out)
-    TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)B * m.vocab * 4, hipMemcpyDeviceToHost));
-  if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)B * 4, hipMemcpyDeviceToHost));
+    TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)s->batch * m.vocab * 4, hipMemcpyDeviceToHost));
+  if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)s->batch * 4, hipMemcpyDeviceToHost));
   const auto t_end = clk::now();
-  if (c->profile) {
-    for (int l = 0; l < m.layers; l++) {
-      float ms = 0;
-      TGOHIP_HIP(hipEventElapsedTime(&ms, c->prof_ev[2 * l], c->prof_ev[2 * l + 1]));
-      c->prof_attn_ms += ms;
-    }
-    c->prof_attn_launches += m.layers;
-    c->prof_attn_bytes += attn_bytes * m.layers;
-  }
+  if ((rc = profile_collect(c, 0, o.attn_bytes))) return rc;
   if (tm) {
     float dev_ms = 0;
     (void)hipEventElapsedTime(&dev_ms, c->ev0, c->ev1);
@@ -1000,7 +1062,29 @@ struct SchedSlot {
   PrefixLease* lease = nullptr;
   std::vector<int> pages;
   int length = 0;
+  // Overlap mode: the books projected past the steps in flight (prompt length
+  // counting generated tokens not yet read back, positions scored, length).
+  int plen_p = 0, pf_p = 0, len_p = 0;
+  int inflight = 0;       // steps in flight holding rows of this slot
+  bool pending = false;   // its next row's token is its entry of the device argmax
+  bool retiring = false;  // finished while rows were in flight: released when they land
 };
+
+// A step submitted in overlap mode and not yet collected.
+struct InflightStep {
+  std::vector<int> ws, wst, wc;  // working slots, prompt start (-1: decode row), rows
+  std::vector<int> row0;         // each working slot's first row
+  std::vector<char> done;        // the slot's prompt is scored once the step lands
+  int parity = 0;
+  int32_t prefill = 0, decodes = 0;
+  double submit_ms = 0, attn_bytes = 0;
+};
+
+static void sync_proj(SchedSlot& s) {
+  s.plen_p = (int)s.prompt.size();
+  s.pf_p = s.prefilled;
+  s.len_p = s.length;
+}
 
 struct tgohip_sched {
   tgohip_ctx* ctx;
@@ -1012,6 +1096,12 @@ struct tgohip_sched {
   std::vector<uint32_t> ids, posq, posk, slotv, lengths, extents, last, table;
   int table_stride = 1;  // row stride of table: the longest lease of the last step
   std::vector<int32_t> argmax;
+  // overlap mode (tgohip_sched_set_overlap)
+  bool overlap = false;
+  std::deque<InflightStep> flight;
+  int parity = 0;
+  hipEvent_t ev[2][3] = {};        // per parity: begin, kernels done, argmax copied
+  int32_t* amax_host[2] = {};      // per parity: pinned copy of the step's argmax
 };
 
 static void slot_release(SchedSlot& s) {
@@ -1057,7 +1147,13 @@ tgohip_sched* tgohip_sched_new(tgohip_ctx* c, int n, int chunk, int reserve, int
 
 void tgohip_sched_free(tgohip_sched* s) {
   if (!s) return;
+  if (!s->flight.empty()) (void)hipStreamSynchronize(s->ctx->stream);
   for (auto& sl : s->slots) slot_release(sl);
+  for (int p = 0; p < 2; p++) {
+    for (hipEvent_t& e : s->ev[p])
+      if (e) (void)hipEventDestroy(e);
+    if (s->amax_host[p]) (void)hipHostFree(s->amax_host[p]);
+  }
   delete s;
 }
 
@@ -1067,7 +1163,7 @@ int tgohip_sched_admit(tgohip_sched* s, const int32_t* prompt, int n, int reserv
   if (n <= 0) return fail(TGOHIP_EINVAL, "the prompt is empty; there is nothing to condition on");
   int free = -1;
   for (int i = 0; i < (int)s->slots.size(); i++)
-    if (!s->slots[i].live) { free = i; break; }
+    if (!s->slots[i].live && s->slots[i].inflight == 0) { free = i; break; }
   if (free < 0) return fail(TGOHIP_ENOSLOT, "every slot is occupied");
   SchedSlot& sl = s->slots[free];
   slot_release(sl);
@@ -1084,6 +1180,7 @@ int tgohip_sched_admit(tgohip_sched* s, const int32_t* prompt, int n, int reserv
   sl.reused = l->reused;
   sl.arrived = s->next;
   sl.feed = 0;
+  sync_proj(sl);
   return free;
 }
 
@@ -1092,6 +1189,12 @@ int tgohip_sched_finish(tgohip_sched* s, int slot) {
     return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " is outside a batch of " +
                                    std::to_string(s->slots.size()));
   SchedSlot& sl = s->slots[slot];
+  if (sl.inflight > 0) {
+    // rows of it are still in flight (overlap mode): they land first
+    sl.live = false;
+    sl.retiring = true;
+    return 0;
+  }
   slot_release(sl);
   sl = SchedSlot();
   return 0;
@@ -1118,6 +1221,10 @@ int tgohip_sched_feed(tgohip_sched* s, int slot, int token) {
                                    std::to_string(s->slots.size()));
   SchedSlot& sl = s->slots[slot];
   if (!sl.live) return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " holds no sequence");
+  if (sl.pending || sl.inflight > 0)
+    return fail(TGOHIP_ESTATE, "slot " + std::to_string(slot) + " has rows in flight or is fed "
+                               "by the device: in overlap mode the scheduler feeds each generated "
+                               "token itself");
   if (sl.prefilled < (int)sl.prompt.size())
     return fail(TGOHIP_EINVAL, "slot " + std::to_string(slot) + " is " + std::to_string(sl.prefilled) +
                                    " tokens into a " + std::to_string(sl.prompt.size()) +
@@ -1129,6 +1236,7 @@ int tgohip_sched_feed(tgohip_sched* s, int slot, int token) {
   sl.feed = token;
   sl.prompt.push_back(token);
   sl.prefilled++;
+  sync_proj(sl);
   return 0;
 }
 
@@ -1139,6 +1247,9 @@ int tgohip_sched_length(tgohip_sched* s, int slot) {
 
 int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, int32_t* out_done,
                       int32_t* prefill_tokens, int32_t* decodes, tgohip_timings* tm) {
+  if (s->overlap)
+    return fail(TGOHIP_ESTATE, "the scheduler is in overlap mode: steps go through "
+                               "tgohip_sched_submit and tgohip_sched_collect");
   const int n = (int)s->slots.size();
   const tgohip_model_cfg& m = s->ctx->cfg;
   std::vector<int32_t> live(n), plen(n), pf(n), ws(n), wst(n), wc(n);
@@ -1225,11 +1336,222 @@ int tgohip_sched_step(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, in
     st.length += (int)tk.size();
     const bool prefill = st.prefilled < (int)st.prompt.size();
     if (prefill) st.prefilled += (int)tk.size();
+    sync_proj(st);
     out_slot[produced] = sl;
     out_token[produced] = s->argmax[sl];
     out_done[produced] = st.prefilled >= (int)st.prompt.size();
     produced++;
   }
+  return produced;
+}
+
+// ---- overlap mode: the next step is submitted before the last is read back
+//
+// tgo's Batch.step packs, uploads, submits, waits and reads back in one call
+// under the model's lock (batch.go:381-437): the device idles while the host
+// schedules. Here submit() enqueues a step and returns at once, and collect()
+// waits for the oldest step in flight and commits it. A decode row's token is
+// the previous step's argmax, read on the device (the argmax array keeps each
+// slot's latest token), so step k+1 can be submitted before step k is read
+// back. posq/posk/slots are derived on the device from the members' lengths,
+// extents and page rows, so only ids and the per-member ports cross PCIe. The
+// staging buffers and events alternate between two sets.
+int tgohip_sched_set_overlap(tgohip_sched* s, int on) {
+  if (!s->flight.empty())
+    return fail(TGOHIP_ESTATE, "steps are in flight; collect them before switching modes");
+  if (on && !s->ev[0][0]) {
+    for (int p = 0; p < 2; p++) {
+      for (hipEvent_t& e : s->ev[p]) TGOHIP_HIP(hipEventCreate(&e));
+      TGOHIP_HIP(hipHostMalloc((void**)&s->amax_host[p], s->slots.size() * 4, hipHostMallocDefault));
+    }
+  }
+  if (on && !s->overlap) {
+    for (auto& sl : s->slots) {
+      if (sl.live && sl.prefilled >= (int)sl.prompt.size() && sl.length >= (int)sl.prompt.size()) {
+        // a decoding slot whose last token the caller fed: the host holds it
+        sl.pending = false;
+      }
+      sync_proj(sl);
+    }
+  }
+  if (!on && s->overlap) {
+    // back to host feeding: each device-fed slot's token is its last history entry
+    for (auto& sl : s->slots) sl.pending = false;
+  }
+  s->overlap = on != 0;
+  return 0;
+}
+
+int tgohip_sched_submit(tgohip_sched* s, int32_t* out_slot, int32_t* out_done,
+                        int32_t* prefill_tokens, int32_t* decodes) {
+  using clk = std::chrono::steady_clock;
+  const auto t0 = clk::now();
+  if (!s->overlap) return fail(TGOHIP_ESTATE, "submit needs overlap mode (tgohip_sched_set_overlap)");
+  if (s->flight.size() >= 2)
+    return fail(TGOHIP_ESTATE, "two steps are in flight; collect one before submitting another");
+  tgohip_ctx* c = s->ctx;
+  const int n = (int)s->slots.size();
+  const tgohip_model_cfg& m = c->cfg;
+  std::vector<int32_t> live(n), plen(n), pf(n), ws(n), wst(n), wc(n);
+  for (int i = 0; i < n; i++) {
+    const SchedSlot& sl = s->slots[i];
+    live[i] = sl.live;
+    plen[i] = sl.plen_p;
+    pf[i] = sl.pf_p;
+  }
+  int32_t nw = 0, npf = 0, ndc = 0;
+  int rc = tgohip_next_step(n, live.data(), plen.data(), pf.data(), s->chunk, s->max_rows, ws.data(),
+                            wst.data(), wc.data(), &nw, &npf, &ndc);
+  if (rc) return rc;
+  *prefill_tokens = npf;
+  *decodes = ndc;
+  if (nw == 0) return 0;
+  InflightStep f;
+  f.parity = s->parity;
+  f.prefill = npf;
+  f.decodes = ndc;
+  std::vector<int32_t> counts(n, 0);
+  std::vector<uint32_t> rowid;  // ids in member order
+  std::vector<std::vector<uint32_t>> wid(n);
+  for (int i = 0; i < nw; i++) {
+    const int sl = ws[i];
+    SchedSlot& st = s->slots[sl];
+    if (wst[i] >= 0) {
+      if (wst[i] + wc[i] > (int)st.prompt.size())
+        return fail(TGOHIP_ESTATE, "slot " + std::to_string(sl) + ": a prompt chunk reaches past "
+                                   "the tokens the host holds");
+      for (int j = 0; j < wc[i]; j++) wid[sl].push_back((uint32_t)st.prompt[wst[i] + j]);
+    } else {
+      wid[sl].push_back(st.pending ? (0x80000000u | (uint32_t)sl) : (uint32_t)st.feed);
+    }
+    const int need = st.len_p + (int)wid[sl].size();
+    if (need > (int)st.lease->ids.size()) {
+      if ((rc = st.lease->grow(need - (int)st.lease->ids.size()))) return rc;
+    }
+    st.pages = st.lease->blocks;
+  }
+  int total = 0, maxp = 1;
+  for (int i = 0; i < n; i++) {
+    counts[i] = (int32_t)wid[i].size();
+    total += counts[i];
+    maxp = std::max(maxp, (int)s->slots[i].pages.size());
+  }
+  s->table_stride = maxp;
+  s->table.assign((size_t)n * maxp, 0u);
+  s->ids.resize(total);
+  s->lengths.resize(n);
+  s->extents.resize(n);
+  s->last.resize(n);
+  s->posq.clear();
+  s->posk.clear();
+  s->slotv.clear();
+  int at = 0;
+  std::vector<int> row0(n, 0);
+  for (int i = 0; i < n; i++) {
+    const SchedSlot& st = s->slots[i];
+    row0[i] = at;
+    for (size_t j = 0; j < st.pages.size(); j++) s->table[(size_t)i * maxp + j] = (uint32_t)st.pages[j];
+    s->lengths[i] = (uint32_t)(st.len_p + counts[i]);
+    s->extents[i] = (uint32_t)counts[i];
+    s->last[i] = counts[i] > 0 ? (uint32_t)(at + counts[i] - 1) : 0u;
+    for (uint32_t id : wid[i]) s->ids[at++] = id;
+  }
+  tgohip_batch_step bs{total, n, maxp, s->ids.data(), nullptr, nullptr, nullptr,
+                       s->lengths.data(), s->extents.data(), s->last.data(), s->table.data()};
+  if ((rc = ensure_activations(c, total, n))) return rc;  // argmax holds n entries from here
+  StepLaunch o;
+  o.feed = (const int32_t*)c->argmax.p;
+  o.keep_idle = 1;
+  o.ev_begin = s->ev[f.parity][0];
+  o.ev_end = s->ev[f.parity][1];
+  o.prof_set = f.parity;
+  if ((rc = step_launch(c, &bs, o))) return rc;
+  TGOHIP_HIP(hipMemcpyAsync(s->amax_host[f.parity], c->argmax.p, (size_t)n * 4,
+                            hipMemcpyDeviceToHost, c->stream));
+  TGOHIP_HIP(hipEventRecord(s->ev[f.parity][2], c->stream));
+  f.attn_bytes = o.attn_bytes;
+  // the books as they will stand once this step lands
+  int produced = 0;
+  for (int i = 0; i < nw; i++) {
+    const int sl = ws[i];
+    SchedSlot& st = s->slots[sl];
+    st.len_p += counts[sl];
+    st.inflight++;
+    if (wst[i] >= 0) st.pf_p += wc[i];
+    const bool gen = st.pf_p >= st.plen_p;
+    if (gen) {  // the step generates a token, fed to the slot's next row
+      st.plen_p++;
+      st.pf_p++;
+      st.pending = true;
+    }
+    f.ws.push_back(sl);
+    f.wst.push_back(wst[i]);
+    f.wc.push_back(counts[sl]);
+    f.row0.push_back(row0[sl]);
+    f.done.push_back(gen ? 1 : 0);
+    out_slot[produced] = sl;
+    out_done[produced] = gen ? 1 : 0;
+    produced++;
+  }
+  f.submit_ms = std::chrono::duration<double, std::milli>(clk::now() - t0).count();
+  s->flight.push_back(std::move(f));
+  s->parity ^= 1;
+  return produced;
+}
+
+int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token, int32_t* out_done,
+                         tgohip_timings* tm) {
+  if (s->flight.empty()) return 0;
+  InflightStep& f = s->flight.front();
+  TGOHIP_HIP(hipEventSynchronize(s->ev[f.parity][2]));
+  const int32_t* amax = s->amax_host[f.parity];
+  int rc = 0;
+  int produced = 0;
+  for (size_t i = 0; i < f.ws.size(); i++) {
+    const int sl = f.ws[i];
+    SchedSlot& st = s->slots[sl];
+    // the rows' tokens: a prompt chunk, or the slot's fed token (one the
+    // device fed was recorded when the step before was collected)
+    std::vector<int32_t> tk;
+    if (f.wst[i] >= 0) tk.assign(st.prompt.begin() + f.wst[i], st.prompt.begin() + f.wst[i] + f.wc[i]);
+    else tk.push_back(st.feed);
+    // the last step submitted keeps its ports (tgohip_sched_last_step): a
+    // device-fed id becomes the token it stood for
+    if (s->flight.size() == 1 && f.wst[i] < 0) s->ids[f.row0[i]] = (uint32_t)st.feed;
+    const int need = st.length + (int)tk.size();
+    if (need > (int)st.lease->ids.size()) {
+      const int extra = need - (int)st.lease->ids.size();
+      if ((rc = st.lease->commit(tk.data() + tk.size() - extra, extra))) return rc;
+    }
+    st.lease->publish(st.length + (int)tk.size());
+    st.pages = st.lease->blocks;
+    st.length += (int)tk.size();
+    if (st.prefilled < (int)st.prompt.size()) st.prefilled += (int)tk.size();
+    const int tok = amax[sl];
+    if (f.done[i]) {  // the generated token joins the history (the device fed it already)
+      st.feed = tok;
+      st.prompt.push_back(tok);
+      st.prefilled++;
+    }
+    out_slot[produced] = sl;
+    out_token[produced] = tok;
+    out_done[produced] = f.done[i];
+    produced++;
+    st.inflight--;
+    if (st.retiring && st.inflight == 0) {
+      slot_release(st);
+      st = SchedSlot();
+    }
+  }
+  if ((rc = profile_collect(s->ctx, f.parity, f.attn_bytes))) return rc;
+  if (tm) {
+    float dev_ms = 0;
+    (void)hipEventElapsedTime(&dev_ms, s->ev[f.parity][0], s->ev[f.parity][1]);
+    tm->submit_ms = f.submit_ms;
+    tm->device_ms = dev_ms;
+    tm->readback_ms = 0;
+  }
+  s->flight.pop_front();
   return produced;
 }
 
@@ -1291,13 +1613,16 @@ int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, 
   // share them (publishing may adopt an identical block already cached).
   sl.lease->publish(n);
   sl.pages = sl.lease->blocks;
+  sync_proj(sl);
   return slot;
 }
 
+// Sequences still being prefilled; in overlap mode, once the steps in flight
+// have landed.
 int tgohip_sched_prefilling(tgohip_sched* s) {
   int k = 0;
   for (auto& sl : s->slots)
-    if (sl.live && sl.prefilled < (int)sl.prompt.size()) k++;
+    if (sl.live && sl.pf_p < sl.plen_p) k++;
   return k;
 }
 
@@ -1315,6 +1640,23 @@ int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32
   *rows = (int32_t)s->ids.size();
   *batch = (int32_t)s->lengths.size();
   *max_pages = s->table_stride;
+  if (s->posq.empty() && !s->ids.empty()) {
+    // an overlap-mode step left these to the device: derive them as it did
+    const tgohip_model_cfg& m = s->ctx->cfg;
+    const int T = (int)s->ids.size(), B = (int)s->lengths.size();
+    s->posq.assign((size_t)T * m.heads, 0u);
+    s->posk.assign((size_t)T * m.kv_heads, 0u);
+    s->slotv.assign(T, 0u);
+    int t = 0;
+    for (int b = 0; b < B; b++)
+      for (uint32_t j = 0; j < s->extents[b]; j++, t++) {
+        const uint32_t p = s->lengths[b] - s->extents[b] + j;
+        s->slotv[t] = s->table[(size_t)b * s->table_stride + p / m.block] * (uint32_t)m.block +
+                      p % (uint32_t)m.block;
+        for (int h = 0; h < m.heads; h++) s->posq[(size_t)t * m.heads + h] = p;
+        for (int h = 0; h < m.kv_heads; h++) s->posk[(size_t)t * m.kv_heads + h] = p;
+      }
+  }
   auto cp = [](uint32_t* dst, const std::vector<uint32_t>& v) {
     if (dst) std::memcpy(dst, v.data(), v.size() * 4);
   };
