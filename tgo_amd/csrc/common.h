@@ -131,18 +131,10 @@ struct QKRopeArgs {
   size_t plane;           // elements per partial plane
   const float* qnorm;     // [128]
   const float* knorm;     // [128]
-  const uint32_t* posq;   // [T*H], or null: derived from the members below
+  const uint32_t* posq;   // [T*H], or null: rowpos holds the row's position
   const uint32_t* posk;   // [T*Hkv]
   const uint32_t* slots;  // [T]
-  // Members, for posq/posk/slots derived on the device: row t belongs to the
-  // last member b with cu[b] <= t, at position lengths[b] - extents[b] +
-  // (t - cu[b]), slot pages[b][p / block] * block + p % block. Rows past
-  // `total` repeat member `pad`'s last position with slot = capacity.
-  const int32_t* cu;
-  const uint32_t* lengths;
-  const uint32_t* extents;
-  const uint32_t* pages;
-  int B, max_pages, block, total, pad;
+  const uint32_t* rowpos; // [T] (derive_rows_kernel) when posq is null
   const double* inv_freq; // [64]: base^(-2i/128), computed once on the host in double
   float* q;               // [T, H, 128]
   half_t* kc;             // layer view [C, Hkv, 128]
@@ -158,6 +150,19 @@ void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, i
                     float eps, void* out, int out_f16, hipStream_t st, const float* part = nullptr,
                     int nsplit = 0, size_t plane = 0);
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st);
+// posq/posk/slots derived on the device from the members (NewBatchStep's
+// values): row cu[b] + j of member b sits at lengths[b] - extents[b] + j; rows
+// past `total` repeat member pad's last position with slot = capacity.
+struct DeriveArgs {
+  const int32_t* cu;
+  const uint32_t* lengths;
+  const uint32_t* extents;
+  const uint32_t* pages;
+  int B, max_pages, block, total, pad, T, capacity;
+  uint32_t* pos;   // [T]
+  uint32_t* slot;  // [T]
+};
+void launch_derive_rows(const DeriveArgs& a, hipStream_t st);
 // keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1).
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
                    hipStream_t st, int keep_idle = 0);

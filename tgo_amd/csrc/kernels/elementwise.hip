@@ -91,60 +91,57 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float* x, const uint32_t* 
 }
 
 
+// The rows' positions and cache slots, as model.NewBatchStep packs them
+// (batch.go:310-340): block b < B writes member b's rows cu[b] + j at position
+// lengths[b] - extents[b] + j, slot pages[b][p / block] * block + p % block;
+// block B writes the padding rows past `total`: member pad's last position,
+// slot = capacity (a dropped write).
+__global__ __launch_bounds__(256) void derive_rows_kernel(DeriveArgs a) {
+  const int b = blockIdx.x;
+  if (b < a.B) {
+    const int n = (int)a.extents[b];
+    const int first = (int)a.lengths[b] - n, t0 = a.cu[b];
+    const uint32_t* prow = a.pages + (size_t)b * a.max_pages;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+      const int p = first + j;
+      a.pos[t0 + j] = (uint32_t)p;
+      a.slot[t0 + j] = prow[p / a.block] * (uint32_t)a.block + (uint32_t)(p % a.block);
+    }
+  } else {
+    const uint32_t p = a.lengths[a.pad] - 1;
+    for (int t = a.total + threadIdx.x; t < a.T; t += blockDim.x) {
+      a.pos[t] = p;
+      a.slot[t] = (uint32_t)a.capacity;
+    }
+  }
+}
+
 // One block (4 waves) per token; a wave takes one head row at a time and a
-// lane owns the rotated pair (2*lane, 2*lane+1).
+// lane owns the rotated pair (2*lane, 2*lane+1). (Loading a batch of a wave's
+// rows before working on any measured 65% slower.)
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int W = (a.H + 2 * a.Hkv) * kHeadDim;
-  const float* row = a.qkv + (size_t)t * W;
-  // split-K projection: the row is the sum of the partial planes, in split order
-  auto load2 = [&](int off) -> float2 {
-    if (a.nsplit == 0) return *(const float2*)(row + off);
-    float2 acc = make_float2(0.f, 0.f);
-    for (int sp = 0; sp < a.nsplit; sp++) {
-      const float2 pv = *(const float2*)(a.qkv + sp * a.plane + (size_t)t * W + off);
-      acc.x += pv.x;
-      acc.y += pv.y;
-    }
-    return acc;
-  };
-  uint32_t slot;
-  int dpos = 0;  // the row's position when derived
-  if (a.slots) {
-    slot = a.slots[t];
-  } else {
-    __shared__ uint32_t sh[2];
-    if (threadIdx.x == 0) {
-      int b, p;
-      uint32_t sl;
-      if (t < a.total) {
-        int lo = 0, hi = a.B - 1;  // the last member with cu[b] <= t
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (a.cu[mid] <= t) lo = mid;
-          else hi = mid - 1;
-        }
-        b = lo;
-        p = (int)a.lengths[b] - (int)a.extents[b] + (t - a.cu[b]);
-        sl = a.pages[(size_t)b * a.max_pages + p / a.block] * (uint32_t)a.block + (uint32_t)(p % a.block);
-      } else {
-        b = a.pad;
-        p = (int)a.lengths[b] - 1;
-        sl = (uint32_t)a.capacity;
-      }
-      sh[0] = (uint32_t)p;
-      sh[1] = sl;
-    }
-    __syncthreads();
-    dpos = (int)sh[0];
-    slot = sh[1];
-  }
+  const uint32_t slot = a.slots[t];
+  const int dpos = a.rowpos ? (int)a.rowpos[t] : 0;  // the row's position when derived
   const bool write = slot < (uint32_t)a.capacity;
   int cpos = -1;
   float c = 1.f, s = 0.f;
   const double inv = a.inv_freq[lane];
   for (int hh = wave; hh < a.H + 2 * a.Hkv; hh += 4) {
-    const float2 v = load2(hh * kHeadDim + 2 * lane);
+    // split-K projection: the row is the sum of the partial planes, in split order
+    const float* row = a.qkv + (size_t)t * W;
+    float2 v;
+    if (a.nsplit == 0) {
+      v = *(const float2*)(row + hh * kHeadDim + 2 * lane);
+    } else {
+      v = make_float2(0.f, 0.f);
+      for (int sp = 0; sp < a.nsplit; sp++) {
+        const float2 pv = *(const float2*)(a.qkv + sp * a.plane + (size_t)t * W + hh * kHeadDim + 2 * lane);
+        v.x += pv.x;
+        v.y += pv.y;
+      }
+    }
     if (hh >= a.H + a.Hkv) {
       // value head: narrowed and scattered as is
       if (write) {
@@ -159,7 +156,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
     const float ss = wave_sum(v.x * v.x + v.y * v.y);
     const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
     const float x0 = v.x * sc * gain[2 * lane], x1 = v.y * sc * gain[2 * lane + 1];
-    const int pos = !a.posq ? dpos
+    const int pos = a.rowpos ? dpos
                     : isq   ? (int)a.posq[(size_t)t * a.H + hh]
                             : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
     if (pos != cpos) {
@@ -357,6 +354,9 @@ void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, i
                     int nsplit, size_t plane) {
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, st, x, rows, g, w, eps, out, out_f16,
                      part, nsplit, plane);
+}
+void launch_derive_rows(const DeriveArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(derive_rows_kernel, dim3(a.B + 1), dim3(256), 0, st, a);
 }
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);

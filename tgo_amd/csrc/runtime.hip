@@ -89,6 +89,7 @@ struct tgohip_ctx {
   int cascade = 0;    // minimum sequences sharing a prefix for prefix-shared attention (0: off)
   // activations and workspaces
   DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, meta, gemm_ws, part_o, part_ml;
+  DevBuf rows;  // [2][rows]: positions and slots derived on the device
   int rows_cap = 0, batch_cap = 0;
   // pinned staging for per-step metadata
   void* pinned = nullptr;
@@ -375,6 +376,7 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
     if ((rc = c->q.ensure(rows * qw * 4))) return rc;
     if ((rc = c->attn.ensure(rows * qw * 4))) return rc;
     if ((rc = c->act.ensure(rows * f * act_el + 256))) return rc;
+    if ((rc = c->rows.ensure((size_t)rows * 8))) return rc;
     c->rows_cap = rows;
   }
   if (B > c->batch_cap) {
@@ -816,6 +818,12 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     pev = c->prof_ev.data() + (size_t)o.prof_set * 2 * m.layers;
   }
   launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
+  uint32_t* d_rowpos = (uint32_t*)c->rows.p;
+  uint32_t* d_rowslot = d_rowpos + T;
+  if (derived)
+    launch_derive_rows(DeriveArgs{dp.cu, dp.lengths, d_ext, dp.pages, B, s->max_pages, m.block,
+                                  plan.claimed, pad, T, c->kv_positions, d_rowpos, d_rowslot},
+                       st);
   // A split-K projection's partial planes are summed by the kernel that reads
   // its output next (in split order, so the result is the reduction's):
   // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
@@ -833,8 +841,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   (size_t)T * (m.heads + 2 * m.kv_heads) * kHeadDim, L.g_q, L.g_k,
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
-                  derived ? nullptr : sg.dev<uint32_t>(c, o_slots),
-                  dp.cu, dp.lengths, d_ext, dp.pages, B, s->max_pages, m.block, plan.claimed, pad,
+                  derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
                   c->inv_freq, (float*)c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps};
     launch_qk_rope_kv(qa, T, st);
