@@ -23,7 +23,8 @@ value = output tokens (sampleable tokens produced) / wall time of the timed
 steps, inputs resident in HBM. The roofline object is the ragged paged
 attention kernel (the metric's "paged-attn HBM GB/s"): algorithmic bytes per
 launch (every cached position a claimed row reads, K+V of the 8 kv heads
-once = 4096 B per position, plus 24 KiB per query row for q in and out)
+once = 4096 B per position, plus 16 KiB per query row for q in and out, both
+f16)
 divided by its duration, bracketed with HIP events on the launch stream over
 the timed steps. cpu_baseline times tgo's CPU path restated (oracle/) on one
 of the timed steps: the step with 1 and with 2 layers, extrapolated to 36.

@@ -5,6 +5,7 @@ BASELINE config 2. Tolerance (written here, derived the way tolerance.go
 derives budgets, relative to max|v| over the attended rows):
     f16 probabilities into the PV MFMA     2^-11      (StoreF16(1))
     q carried as f16 hi+lo                  2^-21 * (1 + max|score|)
+      (an f16 q is exact; its scores are scaled once in f32, inside this term)
     f32 accumulation over d_h and over L    (sqrt(d_h) + sqrt(L)) * 2^-24
     exp2 / division                         8 * 2^-23
 The f16 cache rounding is not charged: the oracle reads the same f16 K/V.
@@ -40,9 +41,9 @@ def pad_heads(x, rows, heads, dh):
 
 
 def run(ctx, torch, q, k16, v16, lengths, extents, pages, max_pages, block, scale, H, Hkv,
-        out_f16=False):
+        out_f16=False, q_f16=False):
     T = q.shape[0]
-    dq = torch.from_numpy(np.ascontiguousarray(q, np.float32)).cuda()
+    dq = torch.from_numpy(np.ascontiguousarray(q, np.float16 if q_f16 else np.float32)).cuda()
     dk = torch.from_numpy(np.ascontiguousarray(k16).view(np.int16)).cuda()
     dv = torch.from_numpy(np.ascontiguousarray(v16).view(np.int16)).cuda()
     cap = k16.shape[0]
@@ -50,7 +51,7 @@ def run(ctx, torch, q, k16, v16, lengths, extents, pages, max_pages, block, scal
                       device="cuda")
     import tgo_amd
     ctx.paged_attention(dq, T, H, Hkv, dk, dv, cap, lengths, extents, pages, max_pages, block,
-                        scale, dout, q_dtype=tgo_amd.F32,
+                        scale, dout, q_dtype=tgo_amd.F16 if q_f16 else tgo_amd.F32,
                         out_dtype=tgo_amd.F16 if out_f16 else tgo_amd.F32)
     torch.cuda.synchronize()
     return dout.float().cpu().numpy()
@@ -238,6 +239,42 @@ def test_c2_mixed_equals_apart_at_full_size(ctx, torch_gpu):
         rows = slice(cu[s], cu[s + 1])
         alone = run(ctx, torch_gpu, c["q"][rows], c["k"], c["v"], [c["L"][s]], [c["ext"][s]],
                     c["pages"][s], c["maxp"], c["block"], c["scale"], c["H"], c["Hkv"])
+        assert np.array_equal(alone, got[rows]), s
+
+
+def test_f16_queries_match_the_oracle(ctx, torch_gpu):
+    """An f16 q (the f16-activation mode's) takes one MFMA per product, the scores
+    scaled in f32 afterwards: against the oracle fed the same f16 values, on the C16
+    probe and on sampled rows of config 2 (decode rows and chunk rows); and mixed
+    equals apart, bit for bit."""
+    g = GOLD["ragged_probe"]
+    q, k16, v16, lengths, extents, pages = probe_inputs(g["seqs"])
+    q16 = q.astype(np.float16)
+    got = run(ctx, torch_gpu, q16, k16, v16, lengths, extents, pages, g["max_pages"], g["block"],
+              g["scale"], g["qheads"], g["kvheads"], q_f16=True)
+    want, b = oracle.ragged_attention_f64(q16.astype(np.float32), g["qheads"], g["kvheads"], DH,
+                                          k16, v16, lengths, extents, pages, g["max_pages"],
+                                          g["block"], g["scale"])
+    assert np.abs(got - want).max() <= budget(b)
+    c = c2_inputs(5)
+    q16 = c["q"].astype(np.float16)
+    got = run(ctx, torch_gpu, q16, c["k"], c["v"], c["L"], c["ext"], c["pages"].ravel(),
+              c["maxp"], c["block"], c["scale"], c["H"], c["Hkv"], q_f16=True)
+    cu = np.concatenate([[0], np.cumsum(c["ext"])])
+    for s in (3, 20, 41, 56, 59, 62):
+        L, n = int(c["L"][s]), int(c["ext"][s])
+        k_tok = min(n, 4)
+        Ls = L - n + k_tok
+        rows = slice(cu[s], cu[s] + k_tok)
+        want, b = oracle.ragged_attention_f64(q16[rows].astype(np.float32), c["H"], c["Hkv"], DH,
+                                              c["k"], c["v"], [Ls], [k_tok], c["pages"][s],
+                                              c["maxp"], c["block"], c["scale"])
+        err = np.abs(got[rows] - want).max()
+        assert err <= budget(b), (s, L, n, err, budget(b))
+    for s in (0, 56, 63):
+        rows = slice(cu[s], cu[s + 1])
+        alone = run(ctx, torch_gpu, q16[rows], c["k"], c["v"], [c["L"][s]], [c["ext"][s]],
+                    c["pages"][s], c["maxp"], c["block"], c["scale"], c["H"], c["Hkv"], q_f16=True)
         assert np.array_equal(alone, got[rows]), s
 
 

@@ -136,11 +136,12 @@ struct QKRopeArgs {
   const uint32_t* slots;  // [T]
   const uint32_t* rowpos; // [T] (derive_rows_kernel) when posq is null
   const double* inv_freq; // [64]: base^(-2i/128), computed once on the host in double
-  float* q;               // [T, H, 128]
+  void* q;                // [T, H, 128], f32 or (q_f16) f16
   half_t* kc;             // layer view [C, Hkv, 128]
   half_t* vc;
   int H, Hkv, capacity;
   float eps;
+  int q_f16;
 };
 // ids[t] with bit 31 set names a member b = ids[t] & 0x7fffffff whose token is
 // feed[b] (the previous step's argmax, left on the device).

@@ -13,8 +13,10 @@
 //    are 256-byte bank rows with 16-byte chunks XOR-swizzled by position; V is
 //    transposed on the way in, its 4-position groups XOR-swizzled by dim row.
 //    Barriers order LDS only, so the next tiles' loads stay in flight.
-//  * q is split into an f16 high and low part (two MFMAs), so the f32 query is
-//    carried to ~2^-22 and the product with the f16 key is accumulated in f32.
+//  * An f32 q is split into an f16 high and low part (two MFMAs), so the f32
+//    query is carried to ~2^-22 and the product with the f16 key is
+//    accumulated in f32. An f16 q takes one MFMA, and the scores are scaled in
+//    f32 afterwards.
 //  * Decode-style items (<= 16 rows: 1 token x G query heads) run S^T = K.Q^T
 //    on v_mfma_f32_16x16x32_f16 and O^T = V^T.P^T on v_mfma_f32_16x16x16_f16
 //    (the D layout of the first is the B layout of the second). The four waves
@@ -218,21 +220,29 @@ __device__ __forceinline__ void attn_store_block(half_t* Kw, half_t* Vw, int dch
   }
 }
 
-// q (f32 or f16) times scale*log2(e), split into an f16 high and low part.
+// f32 q: times scale*log2(e), split into an f16 high and low part (two
+// MFMAs carry about 22 bits). f16 q (QF16): the stored halves as they are, one
+// MFMA; the scores are scaled in f32 instead (attn_qscale), so the product is
+// the exact f32 dot product of the f16 query and key, scaled once.
+template <bool QF16>
 __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool valid, half8_t& hi,
                                             half8_t& lo) {
+  if (QF16) {
+    if (valid) {
+      hi = *(const half8_t*)((const half_t*)a.q + off);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) hi[j] = (half_t)0.f;
+    }
+    lo = hi;  // unused
+    return;
+  }
   float x[8];
   if (valid) {
-    if (a.q_f16) {
-      const half8_t h = *(const half8_t*)((const half_t*)a.q + off);
-#pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = (float)h[j];
-    } else {
-      const float4_t u = *(const float4_t*)((const float*)a.q + off);
-      const float4_t w = *(const float4_t*)((const float*)a.q + off + 4);
-      x[0] = u[0]; x[1] = u[1]; x[2] = u[2]; x[3] = u[3];
-      x[4] = w[0]; x[5] = w[1]; x[6] = w[2]; x[7] = w[3];
-    }
+    const float4_t u = *(const float4_t*)((const float*)a.q + off);
+    const float4_t w = *(const float4_t*)((const float*)a.q + off + 4);
+    x[0] = u[0]; x[1] = u[1]; x[2] = u[2]; x[3] = u[3];
+    x[4] = w[0]; x[5] = w[1]; x[6] = w[2]; x[7] = w[3];
   } else {
 #pragma unroll
     for (int j = 0; j < 8; j++) x[j] = 0.f;
@@ -244,6 +254,14 @@ __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool 
     hi[j] = h;
     lo[j] = (half_t)(xs - (float)h);
   }
+}
+
+// What a raw score is multiplied by to reach log2 units: 1 when q carried the
+// scale in (f32 q), scale*log2(e) for f16 q. Applied as exp2(fma(s, qs, -m))
+// and to the tile maximum, so it costs no instruction per score.
+template <bool QF16>
+__device__ __forceinline__ float attn_qscale(const AttnArgs& a) {
+  return QF16 ? a.qscale : 1.f;
 }
 
 // Tiles of loads a decode-style item keeps in flight (its registers are free:
@@ -266,9 +284,10 @@ constexpr float kLazyMax = 8.f;
 // The four waves take the four 16-position blocks of each 64-position tile and
 // merge their softmax states at the end. kDecodeDepth tiles of loads are in
 // flight.
-template <int BLK>
+template <int BLK, bool QF16>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                             char* smem) {
+  const float qs = attn_qscale<QF16>(a);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   // Wave w owns positions 16w + [0,16) of every tile, in an LDS region of its
@@ -288,7 +307,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
   {
     const size_t qoff = ((size_t)(c.cu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) attn_load_q(a, qoff + 32 * cc + 8 * lg, valid, qh[cc], ql[cc]);
+    for (int cc = 0; cc < 4; cc++) attn_load_q<QF16>(a, qoff + 32 * cc + 8 * lg, valid, qh[cc], ql[cc]);
   }
 
   float m = kNoMax, l = 0.f;
@@ -322,7 +341,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           for (int cc = 0; cc < 4; cc++) {
             const half8_t ka = *(const half8_t*)(Kw + (li * 16 + ((4 * cc + lg) ^ li)) * 8);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[cc], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[cc], acc, 0, 0, 0);
+            if (!QF16) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[cc], acc, 0, 0, 0);
           }
           if (t0 + mb * 16 + 16 <= full_hi && valid) {
             st = acc;
@@ -335,7 +354,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           }
         }
         float tmax = fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3]));
-        tmax = wave_max16x(tmax);
+        tmax = wave_max16x(tmax) * qs;
         // A row that has seen no visible position keeps m = kNoMax and gets
         // p = 0. The MFMAs below run on every lane.
         const bool grow = tmax > m + kLazyMax;
@@ -351,7 +370,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
         half4_t pb;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const float p = __builtin_amdgcn_exp2f(st[q] - m);
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[q], qs, -m));
           psum += p;
           pb[q] = (half_t)p;
         }
@@ -426,9 +445,10 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
 //   16t + (e < 4 ? 4kh + e : 8 + 4kh + e - 4) of the block, which is exactly
 //   where the lane's own probabilities sit (scores i = 8t..8t+7), so P never
 //   leaves registers; the A operand is two 8-byte reads of transposed V.
-template <int BLK>
+template <int BLK, bool QF16>
 __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                              char* smem) {
+  const float qs = attn_qscale<QF16>(a);
   half_t* Ks = (half_t*)smem;
   half_t* Vs = (half_t*)(smem + 16384);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -454,7 +474,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
   {
     const size_t qoff = ((size_t)(rcu + tok) * a.H + head) * kHeadDim;
 #pragma unroll
-    for (int ss = 0; ss < 8; ss++) attn_load_q(a, qoff + 16 * ss + 8 * kh, valid, qh[ss], ql[ss]);
+    for (int ss = 0; ss < 8; ss++) attn_load_q<QF16>(a, qoff + 16 * ss + 8 * kh, valid, qh[ss], ql[ss]);
   }
 
   float m = kNoMax, l = 0.f;
@@ -482,7 +502,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
       for (int ss = 0; ss < 8; ss++) {
         const half8_t ka = *(const half8_t*)(Ks + (pos * 16 + ((2 * ss + kh) ^ (pos & 15))) * 8);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ss], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[ss], acc, 0, 0, 0);
+        if (!QF16) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[ss], acc, 0, 0, 0);
       }
       sc[pb] = acc;
     }
@@ -502,7 +522,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
           tmax = fmaxf(tmax, sc[pb][i]);
         }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * qs;
     const bool grow = tmax > m + kLazyMax;
     if (__builtin_amdgcn_ballot_w64(grow)) {  // uniform across the wave
       const float mnew = grow ? tmax : m;
@@ -518,7 +538,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
     for (int pb = 0; pb < 2; pb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float p = __builtin_amdgcn_exp2f(sc[pb][i] - m);
+        const float p = __builtin_amdgcn_exp2f(fmaf(sc[pb][i], qs, -m));
         psum += p;
         pf[pb][i >> 3][i & 7] = (half_t)p;
       }
@@ -582,7 +602,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
 
 // BLK is the page size when it is 16 (the fast path: a 64-position tile is
 // four whole pages), or 0 for any other page size.
-template <int BLK>
+template <int BLK, bool QF16>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmem];
   const AttnItem it = a.items[blockIdx.x];
@@ -616,9 +636,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     // Decode waves are HBM streams: raised priority lets their loads and short
     // softmax steps issue ahead of a co-resident prefill item's MFMA work.
     __builtin_amdgcn_s_setprio(1);
-    attn_decode<BLK>(a, it, c, smem);
+    attn_decode<BLK, QF16>(a, it, c, smem);
   } else {
-    attn_prefill<BLK>(a, it, c, smem);
+    attn_prefill<BLK, QF16>(a, it, c, smem);
   }
 }
 
@@ -954,10 +974,11 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
   a.G = H / Hkv;
   a.qscale = scale * 1.4426950408889634f;
   if (!plan.items.empty()) {
-    if (block == 16)
-      hipLaunchKernelGGL(attn_kernel<16>, dim3((unsigned)plan.items.size()), dim3(256), 0, stream, a);
-    else
-      hipLaunchKernelGGL(attn_kernel<0>, dim3((unsigned)plan.items.size()), dim3(256), 0, stream, a);
+    const dim3 grid((unsigned)plan.items.size());
+    if (block == 16 && q_f16) hipLaunchKernelGGL((attn_kernel<16, true>), grid, dim3(256), 0, stream, a);
+    else if (block == 16) hipLaunchKernelGGL((attn_kernel<16, false>), grid, dim3(256), 0, stream, a);
+    else if (q_f16) hipLaunchKernelGGL((attn_kernel<0, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((attn_kernel<0, false>), grid, dim3(256), 0, stream, a);
   }
   if (!plan.combines.empty())
     hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)plan.combines.size(), kAttnRowsP / 16),

@@ -166,8 +166,11 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
       cpos = pos;
     }
     const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-    if (isq) {
-      *(float2*)(a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = make_float2(y0, y1);
+    if (isq && a.q_f16) {
+      half2_t hq = {(half_t)y0, (half_t)y1};
+      *(half2_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = hq;
+    } else if (isq) {
+      *(float2*)((float*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = make_float2(y0, y1);
     } else if (write) {
       const int kh = hh - a.H;
       half2_t hk = {(half_t)y0, (half_t)y1};

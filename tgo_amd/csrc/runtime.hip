@@ -808,7 +808,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   if (c->profile) {
     for (int b = 0; b < B; b++)
       if (s->extents[b] > 0) o.attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
-    o.attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (4 + (f32act ? 4 : 2));
+    o.attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (f32act ? 4 + 4 : 2 + 2);  // q in, out
     o.attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
     while ((int)c->prof_ev.size() < 4 * m.layers) {
       hipEvent_t e;
@@ -842,11 +842,11 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
-                  c->inv_freq, (float*)c->q.p, c->kc + l * layer_kv,
-                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps};
+                  c->inv_freq, c->q.p, c->kc + l * layer_kv,
+                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16};
     launch_qk_rope_kv(qa, T, st);
     if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l], st));
-    if ((rc = attn_enqueue(plan, dp, c->q.p, 0, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
+    if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
     if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l + 1], st));
