@@ -84,6 +84,11 @@ __device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const
   }
 }
 
+// One lane's 16-byte chunk of a K or V row. A native vector (not HIP's struct
+// uint4): copies through it are plain loads and stores, so the arrays of
+// chunks a wave keeps in flight stay in registers.
+typedef uint32_t kv16_t __attribute__((ext_vector_type(4)));
+
 constexpr int kMaxItemPages = 1024;        // page indices an item stages in LDS
 constexpr int kAttnVBytes = 20480;         // one V tile in LDS (64 padded rows)
 constexpr int kAttnSmem = 16384 + kAttnVBytes + kMaxItemPages * 4;
@@ -144,7 +149,7 @@ __device__ __forceinline__ uint32_t attn_row_of(const AttnCtx& c, int p) {
 // 8*dch + [0,8). Positions at or past hi load zeros.
 template <int BLK>
 __device__ __forceinline__ void attn_load_tile(const AttnArgs& a, const AttnCtx& c, int t0, int hi,
-                                               uint4 (&kr)[4], uint4 (&vr)[4]) {
+                                               kv16_t (&kr)[4], kv16_t (&vr)[4]) {
   if (BLK == 16 && c.staged && t0 + kAttnTile <= hi && (t0 & 15) == 0) {
     // four whole pages: page i holds K positions t0+16i+pgrp; V's four
     // consecutive positions all sit in page pgrp/4
@@ -153,18 +158,18 @@ __device__ __forceinline__ void attn_load_tile(const AttnArgs& a, const AttnCtx&
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t krow = c.pg[pb + i] * 16u + (uint32_t)c.pgrp;
-      kr[i] = *(const uint4*)(a.k + krow * c.rstride + c.lane_off);
-      vr[i] = *(const uint4*)(a.v + (vrow + i) * c.rstride + c.lane_off);
+      kr[i] = *(const kv16_t*)(a.k + krow * c.rstride + c.lane_off);
+      vr[i] = *(const kv16_t*)(a.v + (vrow + i) * c.rstride + c.lane_off);
     }
     return;
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pk = t0 + c.pgrp + 16 * i, pv = t0 + 4 * c.pgrp + i;
-    kr[i] = pk < hi ? *(const uint4*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
-                    : make_uint4(0, 0, 0, 0);
-    vr[i] = pv < hi ? *(const uint4*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
-                    : make_uint4(0, 0, 0, 0);
+    kr[i] = pk < hi ? *(const kv16_t*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+                    : kv16_t{0u, 0u, 0u, 0u};
+    vr[i] = pv < hi ? *(const kv16_t*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+                    : kv16_t{0u, 0u, 0u, 0u};
   }
 }
 
@@ -172,13 +177,13 @@ __device__ __forceinline__ void attn_load_tile(const AttnArgs& a, const AttnCtx&
 // position, 16-byte chunks XOR-swizzled by position; V row-major in padded
 // rows (v_off).
 __device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, half_t* Vs,
-                                                const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+                                                const kv16_t (&kr)[4], const kv16_t (&vr)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pos = c.pgrp + 16 * i;
-    ((uint4*)Ks)[pos * 16 + (c.dch ^ (pos & 15))] = kr[i];
+    ((kv16_t*)Ks)[pos * 16 + (c.dch ^ (pos & 15))] = kr[i];
     const int pv = 4 * c.pgrp + i;
-    *(uint4*)(Vs + v_off(pv, 8 * c.dch)) = vr[i];
+    *(kv16_t*)(Vs + v_off(pv, 8 * c.dch)) = vr[i];
   }
 }
 
@@ -187,23 +192,33 @@ __device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, ha
 // p0 + 4prow + i, dims 8*dch + [0,8). Positions at or past hi load zeros.
 template <int BLK>
 __device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx& c, int p0, int hi,
-                                                int prow, uint4 (&kr)[4], uint4 (&vr)[4]) {
-  if (BLK == 16 && c.staged && p0 + 16 <= hi && (p0 & 15) == 0) {
-    const uint32_t base = c.pg[(p0 >> 4) - c.pg0] * 16u;  // one whole page
+                                                int prow, kv16_t (&kr)[4], kv16_t (&vr)[4]) {
+  if (BLK == 16) {
+    // Branch-free, so the compiler can count each block's loads and wait for
+    // the oldest block only (with branches here it waits for every load in
+    // flight). The page table is staged in LDS (the host splits items so that
+    // it always is). Positions at or past hi read position hi - 1: finite
+    // values whose scores the caller masks, so their probabilities are zero.
+    const int last = hi - 1;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      kr[i] = *(const uint4*)(a.k + (base + (uint32_t)(prow + 4 * i)) * c.rstride + c.lane_off);
-      vr[i] = *(const uint4*)(a.v + (base + (uint32_t)(4 * prow + i)) * c.rstride + c.lane_off);
+      const int pk = min(p0 + prow + 4 * i, last), pv = min(p0 + 4 * prow + i, last);
+      const int ik = min((pk >> 4) - c.pg0, kMaxItemPages - 1);
+      const int iv = min((pv >> 4) - c.pg0, kMaxItemPages - 1);
+      const uint32_t krow = c.pg[ik] * 16u + (uint32_t)(pk & 15);
+      const uint32_t vrow = c.pg[iv] * 16u + (uint32_t)(pv & 15);
+      kr[i] = *(const kv16_t*)(a.k + krow * c.rstride + c.lane_off);
+      vr[i] = *(const kv16_t*)(a.v + vrow * c.rstride + c.lane_off);
     }
     return;
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pk = p0 + prow + 4 * i, pv = p0 + 4 * prow + i;
-    kr[i] = pk < hi ? *(const uint4*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
-                    : make_uint4(0, 0, 0, 0);
-    vr[i] = pv < hi ? *(const uint4*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
-                    : make_uint4(0, 0, 0, 0);
+    kr[i] = pk < hi ? *(const kv16_t*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+                    : kv16_t{0u, 0u, 0u, 0u};
+    vr[i] = pv < hi ? *(const kv16_t*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+                    : kv16_t{0u, 0u, 0u, 0u};
   }
 }
 
@@ -211,12 +226,12 @@ __device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx
 // attn_store_tile, V rows at the v_off pitch). Only this wave reads it, and a
 // wave's LDS operations complete in order, so no barrier is needed.
 __device__ __forceinline__ void attn_store_block(half_t* Kw, half_t* Vw, int dch, int prow,
-                                                 const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+                                                 const kv16_t (&kr)[4], const kv16_t (&vr)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pk = prow + 4 * i;
-    ((uint4*)Kw)[pk * 16 + (dch ^ pk)] = kr[i];
-    *(uint4*)(Vw + v_off(4 * prow + i, 8 * dch)) = vr[i];
+    ((kv16_t*)Kw)[pk * 16 + (dch ^ pk)] = kr[i];
+    *(kv16_t*)(Vw + v_off(4 * prow + i, 8 * dch)) = vr[i];
   }
 }
 
@@ -262,6 +277,17 @@ __device__ __forceinline__ void attn_load_q(const AttnArgs& a, size_t off, bool 
 template <bool QF16>
 __device__ __forceinline__ float attn_qscale(const AttnArgs& a) {
   return QF16 ? a.qscale : 1.f;
+}
+
+// f(std::integral_constant<int, i>) for i = 0..N-1, in order: loop indices that
+// are constants from the start, so arrays indexed by them stay in registers
+// whatever the unroller decides.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
 }
 
 // Tiles of loads a decode-style item keeps in flight (its registers are free:
@@ -318,19 +344,25 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
 
   constexpr int D = kDecodeDepth;
   const int wofs = 16 * wave;
-  uint4 kr[D][4], vr[D][4];
-#pragma unroll
-  for (int u = 0; u < D; u++)
-    if (it.kv_lo + u * kAttnTile < it.kv_hi)
+  kv16_t kr[D][4], vr[D][4];
+  // With page 16 the block loads are issued unconditionally, the ones past the
+  // item's end reading its last position again (cache hits): every step then
+  // issues the same loads, the compiler can count them, and a step waits for
+  // its own block only, with D - 1 blocks still in flight.
+  constexpr bool kAlways = BLK == 16;
+  static_for<D>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    if (kAlways || it.kv_lo + u * kAttnTile < it.kv_hi)
       attn_load_block<BLK>(a, c, it.kv_lo + u * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
+  });
   for (int tt = it.kv_lo; tt < it.kv_hi; tt += D * kAttnTile) {
-#pragma unroll
-    for (int u = 0; u < D; u++) {
+    static_for<D>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
       const int t0 = tt + u * kAttnTile;
+      if (t0 < it.kv_hi) attn_store_block(Kw, Vw, li, lg, kr[u], vr[u]);
+      if (kAlways || t0 + D * kAttnTile < it.kv_hi)
+        attn_load_block<BLK>(a, c, t0 + D * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
       if (t0 < it.kv_hi) {
-        attn_store_block(Kw, Vw, li, lg, kr[u], vr[u]);
-        if (t0 + D * kAttnTile < it.kv_hi)
-          attn_load_block<BLK>(a, c, t0 + D * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
 
         // Scores of this wave's 16-position block.
         const int mb = wave;
@@ -385,7 +417,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           }
         }
       }
-    }
+    });
   }
 
   // Merge the four waves' partial softmax states for the (up to) 16 rows.
@@ -484,7 +516,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
 #pragma unroll
     for (int i = 0; i < 16; i++) o[db][i] = 0.f;
 
-  uint4 kr[4], vr[4];
+  kv16_t kr[4], vr[4];
   if (it.kv_lo < it.kv_hi) attn_load_tile<BLK>(a, c, it.kv_lo, it.kv_hi, kr, vr);
   for (int t0 = it.kv_lo; t0 < it.kv_hi; t0 += kAttnTile) {
     attn_lds_barrier();
@@ -744,14 +776,17 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
   // shorter parts spread a chunk's work over more workgroups. Both depend only
   // on the sequence itself, so a mixed launch decomposes every sequence as it
   // would alone. TGOHIP_ATTN_SPLIT / TGOHIP_ATTN_PSPLIT override them.
+  // An override is capped so that a part's page-16 table always fits the
+  // kMaxItemPages the kernel stages in LDS.
+  static constexpr int kSplitCap = (kMaxItemPages - 4) * 16 / kAttnTile * kAttnTile;
   static const int split = [] {
     const char* e = getenv("TGOHIP_ATTN_SPLIT");
-    const int v = e ? atoi(e) : kAttnSplitDecode;
+    const int v = std::min(e ? atoi(e) : kAttnSplitDecode, kSplitCap);
     return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplitDecode;
   }();
   static const int psplit = [] {
     const char* e = getenv("TGOHIP_ATTN_PSPLIT");
-    const int v = e ? atoi(e) : kAttnSplitPrefill;
+    const int v = std::min(e ? atoi(e) : kAttnSplitPrefill, kSplitCap);
     return v >= kAttnTile ? v / kAttnTile * kAttnTile : kAttnSplitPrefill;
   }();
   // Shared prefixes (opt-in): decode sequences (one token) whose page rows
