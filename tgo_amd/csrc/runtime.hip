@@ -440,7 +440,8 @@ tgohip_ctx* tgohip_open(int device) {
   c->ncu = prop.multiProcessorCount;
   if (hipStreamCreate(&c->own_stream) != hipSuccess ||
       hipEventCreateWithFlags(&c->staged, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+      hipEventCreateWithFlags(&c->ev0, hipEventDisableSystemFence) != hipSuccess ||
+      hipEventCreate(&c->ev1) != hipSuccess) {
     fail(TGOHIP_EDEVICE, "tgohip_open: stream/event creation failed");
     delete c;
     return nullptr;
@@ -811,8 +812,10 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     o.attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (f32act ? 4 + 4 : 2 + 2);  // q in, out
     o.attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
     while ((int)c->prof_ev.size() < 4 * m.layers) {
+      // timing only: no system-scope fence (an L2 write-back each, which
+      // left a ~6 us gap on both sides of every attention launch)
       hipEvent_t e;
-      TGOHIP_HIP(hipEventCreate(&e));
+      TGOHIP_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
       c->prof_ev.push_back(e);
     }
     pev = c->prof_ev.data() + (size_t)o.prof_set * 2 * m.layers;
@@ -1368,7 +1371,11 @@ int tgohip_sched_set_overlap(tgohip_sched* s, int on) {
     return fail(TGOHIP_ESTATE, "steps are in flight; collect them before switching modes");
   if (on && !s->ev[0][0]) {
     for (int p = 0; p < 2; p++) {
-      for (hipEvent_t& e : s->ev[p]) TGOHIP_HIP(hipEventCreate(&e));
+      // begin and kernels-done mark timing only; the third (argmax copied)
+      // precedes a host read and keeps the system-scope fence
+      TGOHIP_HIP(hipEventCreateWithFlags(&s->ev[p][0], hipEventDisableSystemFence));
+      TGOHIP_HIP(hipEventCreateWithFlags(&s->ev[p][1], hipEventDisableSystemFence));
+      TGOHIP_HIP(hipEventCreate(&s->ev[p][2]));
       TGOHIP_HIP(hipHostMalloc((void**)&s->amax_host[p], s->slots.size() * 4, hipHostMallocDefault));
     }
   }
