@@ -26,8 +26,10 @@ launch (every cached position a claimed row reads, K+V of the 8 kv heads
 once = 4096 B per position, plus 16 KiB per query row for q in and out, both
 f16)
 divided by its duration, bracketed with HIP events on the launch stream over
-the timed steps. cpu_baseline times tgo's CPU path restated (oracle/) on one
-of the timed steps: the step with 1 and with 2 layers, extrapolated to 36.
+the timed steps (the launches of every 4th layer: each layer's attention does
+the same work, and each event record leaves the device idle a few us).
+cpu_baseline times tgo's CPU path restated (oracle/) on one of the timed
+steps: the step with 1 and with 2 layers, extrapolated to 36.
 """
 import argparse
 import json
@@ -57,6 +59,7 @@ C5_DECODERS = 256
 C5_CHUNK = 1024
 C5_POOL = 330_000       # positions (86 GB of f16 K+V at 64 layers)
 HBM_PEAK = 8000.0       # GB/s, MI355X published
+PROFILE_STRIDE = 4      # attention launches timed: those of every 4th layer
 MFMA_F16_PEAK = 2500.0  # TFLOP/s dense f16, MI355X published
 
 
@@ -220,7 +223,9 @@ def run_steps(wl, ctx, steps, warmup, sync):
 
     run(warmup, False)
     ctx.sync()
-    ctx.set_profile(True)
+    # HIP events around the attention launch of every 4th layer (each layer's
+    # attention does the same work; each record leaves the device idle ~4 us)
+    ctx.set_profile(True, PROFILE_STRIDE)
     t0 = time.perf_counter()
     out, pf, dc, dev_ms = run(steps, True)
     ctx.sync()

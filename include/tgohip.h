@@ -320,10 +320,13 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
                          int32_t* out_done, tgohip_timings* t);
 
 /* ---- measurement ------------------------------------------------------- */
-/* Brackets every attention launch of tgohip_step with HIP events on the
- * context's stream and accumulates its duration and its algorithmic bytes
+/* Brackets the attention launches of tgohip_step with HIP events on the
+ * context's stream and accumulates their duration and algorithmic bytes
  * (every cached position a claimed row reads, K and V of all kv heads, once;
- * plus q read and the output written). Turning it on resets the sums. */
+ * plus q read and the output written). on = 0: off; on = k >= 1: the launch
+ * of every k-th layer (every layer's attention does the same work in a step;
+ * each event record leaves the device idle a few microseconds). Turning it on
+ * resets the sums. */
 int tgohip_set_profile(tgohip_ctx* ctx, int on);
 int tgohip_profile_read(tgohip_ctx* ctx, double* attn_ms, double* attn_bytes,
                         int64_t* launches);

@@ -480,8 +480,9 @@ class Context:
     def kv_synth(self, seed, sigma, positions):
         check(lib().tgohip_kv_synth(self.h, seed, sigma, positions))
 
-    def set_profile(self, on):
-        check(lib().tgohip_set_profile(self.h, 1 if on else 0))
+    def set_profile(self, on, stride=1):
+        """Time the attention launch of every `stride`-th layer (HIP events)."""
+        check(lib().tgohip_set_profile(self.h, stride if on else 0))
 
     def profile_read(self):
         ms, by, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()

@@ -101,6 +101,7 @@ struct tgohip_ctx {
   int next_handle = 1;
   // profiling: HIP events around every attention launch of a step
   bool profile = false;
+  int prof_stride = 1;  // time the attention launch of every prof_stride-th layer
   std::vector<hipEvent_t> prof_ev;
   double prof_attn_ms = 0, prof_attn_bytes = 0;
   int64_t prof_attn_launches = 0;
@@ -848,11 +849,12 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16};
     launch_qk_rope_kv(qa, T, st);
-    if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l], st));
+    const bool timed = pev && l % c->prof_stride == 0;
+    if (timed) TGOHIP_HIP(hipEventRecord(pev[2 * l], st));
     if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
-    if (pev) TGOHIP_HIP(hipEventRecord(pev[2 * l + 1], st));
+    if (timed) TGOHIP_HIP(hipEventRecord(pev[2 * l + 1], st));
     if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
@@ -879,13 +881,14 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
 int profile_collect(tgohip_ctx* c, int prof_set, double attn_bytes) {
   if (!c->profile || c->prof_ev.size() < (size_t)4 * c->cfg.layers) return 0;
   const hipEvent_t* pev = c->prof_ev.data() + (size_t)prof_set * 2 * c->cfg.layers;
-  for (int l = 0; l < c->cfg.layers; l++) {
+  int timed = 0;
+  for (int l = 0; l < c->cfg.layers; l += c->prof_stride, timed++) {
     float ms = 0;
     TGOHIP_HIP(hipEventElapsedTime(&ms, pev[2 * l], pev[2 * l + 1]));
     c->prof_attn_ms += ms;
   }
-  c->prof_attn_launches += c->cfg.layers;
-  c->prof_attn_bytes += attn_bytes * c->cfg.layers;
+  c->prof_attn_launches += timed;
+  c->prof_attn_bytes += attn_bytes * timed;
   return 0;
 }
 
@@ -1577,7 +1580,9 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
 extern "C" {
 
 int tgohip_set_profile(tgohip_ctx* c, int on) {
+  if (on < 0) return fail(TGOHIP_EINVAL, "profile: " + std::to_string(on) + " is not a layer stride");
   c->profile = on != 0;
+  c->prof_stride = on > 0 ? on : 1;
   c->prof_attn_ms = 0;
   c->prof_attn_bytes = 0;
   c->prof_attn_launches = 0;
