@@ -116,65 +116,80 @@ __global__ __launch_bounds__(256) void derive_rows_kernel(DeriveArgs a) {
   }
 }
 
-// One block (4 waves) per token; a wave takes one head row at a time and a
-// lane owns the rotated pair (2*lane, 2*lane+1). (Loading a batch of a wave's
-// rows before working on any measured 65% slower.)
+// Sum over the 32 lanes of a half wave (lanes 0-31 and 32-63 separately).
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One block (4 waves) per token. A wave takes two head rows at a time (lanes
+// 0-31 head 2k, lanes 32-63 head 2k+1, wave w taking k = w, w+4, ...); a lane
+// owns four consecutive dims, the rotated pairs (4l, 4l+1) and (4l+2, 4l+3),
+// with 16-byte loads. (Loading a batch of a wave's rows before working on any
+// measured 65% slower.)
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int W = (a.H + 2 * a.Hkv) * kHeadDim;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int NH = a.H + 2 * a.Hkv;
+  const int W = NH * kHeadDim;
   const uint32_t slot = a.slots[t];
   const int dpos = a.rowpos ? (int)a.rowpos[t] : 0;  // the row's position when derived
   const bool write = slot < (uint32_t)a.capacity;
   int cpos = -1;
-  float c = 1.f, s = 0.f;
-  const double inv = a.inv_freq[lane];
-  for (int hh = wave; hh < a.H + 2 * a.Hkv; hh += 4) {
+  float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
+  const double inv0 = a.inv_freq[2 * l32], inv1 = a.inv_freq[2 * l32 + 1];
+  for (int k = wave; 2 * k < NH; k += 4) {
+    const int hh = 2 * k + half;
+    if (hh >= NH) continue;  // an odd head count leaves the last half wave idle
     // split-K projection: the row is the sum of the partial planes, in split order
-    const float* row = a.qkv + (size_t)t * W;
-    float2 v;
+    const size_t off = (size_t)t * W + hh * kHeadDim + 4 * l32;
+    float4_t v;
     if (a.nsplit == 0) {
-      v = *(const float2*)(row + hh * kHeadDim + 2 * lane);
+      v = *(const float4_t*)(a.qkv + off);
     } else {
-      v = make_float2(0.f, 0.f);
-      for (int sp = 0; sp < a.nsplit; sp++) {
-        const float2 pv = *(const float2*)(a.qkv + sp * a.plane + (size_t)t * W + hh * kHeadDim + 2 * lane);
-        v.x += pv.x;
-        v.y += pv.y;
-      }
+      v = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < a.nsplit; sp++) v += *(const float4_t*)(a.qkv + sp * a.plane + off);
     }
     if (hh >= a.H + a.Hkv) {
       // value head: narrowed and scattered as is
       if (write) {
         const int vh = hh - a.H - a.Hkv;
-        half2_t hv = {(half_t)v.x, (half_t)v.y};
-        *(half2_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHeadDim + 2 * lane) = hv;
+        const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+        *(half4_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHeadDim + 4 * l32) = hv;
       }
       continue;
     }
     const bool isq = hh < a.H;
     const float* gain = isq ? a.qnorm : a.knorm;
-    const float ss = wave_sum(v.x * v.x + v.y * v.y);
+    const float ss = half_wave_sum(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
     const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
-    const float x0 = v.x * sc * gain[2 * lane], x1 = v.y * sc * gain[2 * lane + 1];
+    const float4_t g = *(const float4_t*)(gain + 4 * l32);
+    const float x0 = v[0] * sc * g[0], x1 = v[1] * sc * g[1];
+    const float x2 = v[2] * sc * g[2], x3 = v[3] * sc * g[3];
     const int pos = a.rowpos ? dpos
                     : isq   ? (int)a.posq[(size_t)t * a.H + hh]
                             : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
     if (pos != cpos) {
-      const double ang = (double)pos * inv;
-      c = (float)cos(ang);
-      s = (float)sin(ang);
+      const double ang0 = (double)pos * inv0, ang1 = (double)pos * inv1;
+      c0 = (float)cos(ang0);
+      s0 = (float)sin(ang0);
+      c1 = (float)cos(ang1);
+      s1 = (float)sin(ang1);
       cpos = pos;
     }
-    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    const float y0 = x0 * c0 - x1 * s0, y1 = x0 * s0 + x1 * c0;
+    const float y2 = x2 * c1 - x3 * s1, y3 = x2 * s1 + x3 * c1;
     if (isq && a.q_f16) {
-      half2_t hq = {(half_t)y0, (half_t)y1};
-      *(half2_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = hq;
+      const half4_t hq = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+      *(half4_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) = hq;
     } else if (isq) {
-      *(float2*)((float*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 2 * lane) = make_float2(y0, y1);
+      *(float4_t*)((float*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) =
+          float4_t{y0, y1, y2, y3};
     } else if (write) {
       const int kh = hh - a.H;
-      half2_t hk = {(half_t)y0, (half_t)y1};
-      *(half2_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHeadDim + 2 * lane) = hk;
+      const half4_t hk = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+      *(half4_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHeadDim + 4 * l32) = hk;
     }
   }
 }
