@@ -214,3 +214,26 @@ def test_overlap_refusals(torch_gpu):
     s.set_overlap(False)
     s.close()
     ctx.close()
+
+
+def test_profile_times_every_kth_layer(torch_gpu):
+    """tgohip_set_profile(ctx, k) brackets the attention launch of every k-th layer: the
+    launch count and the algorithmic bytes follow k, and a negative k is refused."""
+    torch = torch_gpu
+    st, table, max_pages = packed_step(np.random.default_rng(9), 0)
+    ctx = new_ctx(torch)
+    counts = {}
+    for k in (1, 2):
+        ctx.set_profile(True, k)
+        for _ in range(3):
+            ctx.step(st, table, max_pages)
+        ms, nbytes, launches = ctx.profile_read()
+        counts[k] = (launches, nbytes)
+        assert ms > 0
+    ctx.set_profile(False)
+    assert counts[1][0] == 3 * CFG["layers"]
+    assert counts[2][0] == 3 * ((CFG["layers"] + 1) // 2)
+    assert counts[1][1] / counts[1][0] == counts[2][1] / counts[2][0]
+    with pytest.raises(tgo_amd.TgoError, match="layer stride"):
+        ctx.set_profile(True, -1)
+    ctx.close()
