@@ -125,6 +125,13 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
                  int max_pages, int block, float scale, hipStream_t stream);
 
 // ---- per-row kernels (kernels/elementwise.hip) ---------------------------
+// Elements between consecutive split-K partial planes of an [M, N] f32
+// product: M*N rounded up to whole 2 MiB pages, so each plane starts on a page.
+inline size_t split_plane_stride(int M, int N) {
+  const size_t e = (size_t)M * N, page = ((size_t)2 << 20) / sizeof(float);
+  return (e + page - 1) / page * page;
+}
+
 struct QKRopeArgs {
   const float* qkv;       // [T, (H + 2*Hkv) * 128], or nsplit partial planes of it
   int nsplit;             // 0: qkv is the projection; > 0: sum the planes (split order)

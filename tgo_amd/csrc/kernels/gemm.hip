@@ -40,7 +40,8 @@ struct GemmArgs {
   const half_t* ws;     // packed scales (form dependent)
   const half_t* wz;     // packed zero+1024 (I4_TGO only)
   void* y;              // output (EPI dependent)
-  float* part;          // split-K partials [splits][M][N]
+  float* part;          // split-K partials: split s at part + s * pstride, [M][N]
+  size_t pstride;
   int M, K, N;
   int ksteps_per_split;
 };
@@ -208,7 +209,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const float16_t
       const int row = m0 + mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if (row >= g.M) continue;
       if (split) {
-        float* dst = g.part + ((size_t)z * g.M + row) * g.N;
+        float* dst = g.part + (size_t)z * g.pstride + (size_t)row * g.N;
 #pragma unroll
         for (int b = 0; b < 2; b++)
           if (nbv[b]) dst[(nbw0 + b) * 32 + c32] = acc[mb][b][r];
@@ -608,7 +609,7 @@ __global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)g.M * outN) return;
   const int row = (int)(i / outN), col = (int)(i % outN);
-  const size_t plane = (size_t)g.M * g.N;
+  const size_t plane = g.pstride;
   if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
     const int gc = (col / 32) * 64 + (col % 32), uc = gc + 32;
     float ga = 0.f, ua = 0.f;
@@ -1032,7 +1033,7 @@ size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
   int mw, nw, tiles_n, tiles, ps;
   pipe_shape(w, M, ncu, mw, nw, tiles_n, tiles, ps);
   s = std::max(s, ps);
-  return s > 1 ? (size_t)s * M * w.N * sizeof(float) : 0;
+  return s > 1 ? (size_t)s * split_plane_stride(M, w.N) * sizeof(float) : 0;
 }
 
 template <int FORM, int MW, int NW>
@@ -1074,9 +1075,10 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
   g.ksteps_per_split = ((KS + splits - 1) / splits + 3) / 4 * 4;
   splits = (KS + g.ksteps_per_split - 1) / g.ksteps_per_split;
   if (splits > 1) {
-    if (!workspace || ws_bytes < (size_t)splits * M * w.N * sizeof(float))
+    if (!workspace || ws_bytes < (size_t)splits * split_plane_stride(M, w.N) * sizeof(float))
       return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
     g.part = workspace;
+    g.pstride = split_plane_stride(M, w.N);
   }
   const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
   switch (w.form) {
@@ -1155,9 +1157,10 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
   const int KS = w.K / 64;
   g.ksteps_per_split = (KS + splits - 1) / splits;
   if (splits > 1) {
-    if (!workspace || ws_bytes < (size_t)splits * M * w.N * sizeof(float))
+    if (!workspace || ws_bytes < (size_t)splits * split_plane_stride(M, w.N) * sizeof(float))
       return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
     g.part = workspace;
+    g.pstride = split_plane_stride(M, w.N);
   }
   const dim3 grid((unsigned)((w.N / 32 + 7) / 8), (unsigned)((M + MW - 1) / MW), (unsigned)splits);
   if (MW == 32) {

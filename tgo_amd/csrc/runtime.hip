@@ -839,7 +839,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   // its output next (in split order, so the result is the reduction's):
   // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
   // rmsnorm. `pend` counts the planes of a residual add still owed to h.
-  const size_t plane = (size_t)T * m.hidden;
+  const size_t plane = split_plane_stride(T, m.hidden);
   int pend = 0;
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
@@ -849,7 +849,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                            &qkv_split)))
       return rc;
     QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
-                  (size_t)T * (m.heads + 2 * m.kv_heads) * kHeadDim, L.g_q, L.g_k,
+                  split_plane_stride(T, (m.heads + 2 * m.kv_heads) * kHeadDim), L.g_q, L.g_k,
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
