@@ -46,10 +46,7 @@ sys.path.insert(0, ROOT)
 C4 = dict(layers=36, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=151936,
           rms_eps=1e-6, rope_theta=1e6, block=16)
 SEED = 2026
-# positions in the shared KV pool (59 GB of f16 K+V): a multiple of 1024, so that
-# each layer's K and V slice (positions x 8 kv heads x 256 B) is whole 2 MiB pages
-# (one layer per page boundary measured 4% faster attention than 400,000)
-POOL = 401_408
+POOL = 400_000          # positions in the shared KV pool (59 GB of f16 K+V)
 SLOTS = 136             # 128 decoders + 2 prefilling + headroom
 CHUNK = 512
 DECODERS = 128
@@ -60,7 +57,7 @@ C5 = dict(layers=64, hidden=5120, heads=64, kv_heads=8, head_dim=128, ffn=25600,
 C5_PREFIX = 2048        # tokens every sequence begins with (128 shared pages)
 C5_DECODERS = 256
 C5_CHUNK = 1024
-C5_POOL = 330_752       # positions (86 GB of f16 K+V at 64 layers; a multiple of 1024)
+C5_POOL = 330_000       # positions (86 GB of f16 K+V at 64 layers)
 HBM_PEAK = 8000.0       # GB/s, MI355X published
 PROFILE_STRIDE = 4      # attention launches timed: those of every 4th layer
 MFMA_F16_PEAK = 2500.0  # TFLOP/s dense f16, MI355X published
