@@ -471,7 +471,8 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
 // rows 32w + [0,32) and every wave consumes every staged tile.
 //   S^T = K . Q^T on v_mfma_f32_32x32x16_f16: A = K (32 positions x 16 dims,
 //   lane (p, kh) reads position p, dims 16s + 8kh + [0,8)), B = Q^T from
-//   registers (hi + lo). Lane (r, kh) gets the scores of row r at positions
+//   registers (hi + lo for an f32 q, the f16 q itself with QF16). Lane (r, kh)
+//   gets the scores of row r at positions
 //   8(i/4) + 4kh + i%4, i = 0..15, of each 32-position block.
 //   O^T += V^T . P^T on the same MFMA: its k index 8kh + e maps to position
 //   16t + (e < 4 ? 4kh + e : 8 + 4kh + e - 4) of the block, which is exactly
