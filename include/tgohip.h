@@ -287,7 +287,10 @@ int tgohip_sched_admit_prefilled(tgohip_sched* s, const int32_t* prompt, int n, 
 int tgohip_sched_prefilling(tgohip_sched* s); /* live slots still mid-prefill */
 int tgohip_sched_live(tgohip_sched* s);       /* live slots */
 /* The ports of the last step (Batch.step's packing): sizes first with NULL
- * arrays, then the arrays (rows, rows*H, rows*H_kv, rows, B, B, B, B*max_pages). */
+ * arrays, then the arrays (rows, rows*H, rows*H_kv, rows, B, B, B, B*max_pages).
+ * In overlap mode, after the last step submitted has been collected (refused
+ * while a step is in flight); posq/posk/slots are then derived on the host as
+ * the device derived them. */
 int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32_t* max_pages,
                            uint32_t* ids, uint32_t* posq, uint32_t* posk, uint32_t* slots,
                            uint32_t* lengths, uint32_t* extents, uint32_t* last,

@@ -202,6 +202,8 @@ def test_overlap_refusals(torch_gpu):
     s.submit()
     with pytest.raises(tgo_amd.TgoError, match="two steps are in flight"):
         s.submit()
+    with pytest.raises(tgo_amd.TgoError, match="a step is in flight"):
+        s.last_step()
     # a slot finished with rows in flight is not reused until they land
     s.finish(slot)
     with pytest.raises(tgo_amd.TgoError):

@@ -580,8 +580,8 @@ class Scheduler:
         """The ports of the last step: (dict of arrays, pages, max_pages)."""
         r, b, mp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
         L = lib()
-        L.tgohip_sched_last_step(self.h, ctypes.byref(r), ctypes.byref(b), ctypes.byref(mp),
-                                 *([None] * 8))
+        check(L.tgohip_sched_last_step(self.h, ctypes.byref(r), ctypes.byref(b),
+                                       ctypes.byref(mp), *([None] * 8)))
         cfg = self.ctx.cfg
         rows, B, maxp = r.value, b.value, mp.value
         st = dict(ids=np.zeros(rows, np.uint32), posq=np.zeros(rows * cfg["heads"], np.uint32),

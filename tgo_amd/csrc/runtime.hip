@@ -1545,7 +1545,10 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
     const int need = st.length + (int)tk.size();
     if (need > (int)st.lease->ids.size()) {
       const int extra = need - (int)st.lease->ids.size();
-      if ((rc = st.lease->commit(tk.data() + tk.size() - extra, extra))) return rc;
+      if ((rc = st.lease->commit(tk.data() + tk.size() - extra, extra))) {
+        s->flight.pop_front();  // the step landed; its books cannot be completed
+        return rc;
+      }
     }
     st.lease->publish(st.length + (int)tk.size());
     st.pages = st.lease->blocks;
@@ -1663,6 +1666,9 @@ int tgohip_sched_live(tgohip_sched* s) {
 int tgohip_sched_last_step(tgohip_sched* s, int32_t* rows, int32_t* batch, int32_t* max_pages,
                            uint32_t* ids, uint32_t* posq, uint32_t* posk, uint32_t* slots,
                            uint32_t* lengths, uint32_t* extents, uint32_t* last, uint32_t* pages) {
+  if (!s->flight.empty())
+    return fail(TGOHIP_ESTATE, "last step: a step is in flight; its ids name device tokens "
+                               "until it is collected");
   *rows = (int32_t)s->ids.size();
   *batch = (int32_t)s->lengths.size();
   *max_pages = s->table_stride;
