@@ -687,22 +687,27 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     // parts in merge order: the shared prefix's (at row xrow + row), then the
     // sequence's own (at row)
     const int np = cb.xparts + cb.nparts;
-    float mstar = -INFINITY;
+    // One pass in part order: a part's (m, l, o) are read together (no load
+    // waits for an earlier part's) and folded into a running state kept at
+    // the running maximum, as an online softmax folds tiles.
+    float m = -INFINITY, lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int p = 0; p < np; p++) {
       const size_t part = (size_t)(p < cb.xparts ? cb.xpart0 + p : cb.part0 + p - cb.xparts);
       const int pr = p < cb.xparts ? cb.xrow + row : row;
-      mstar = fmaxf(mstar, a.part_ml[part * 2 * kAttnRowsP + pr]);
-    }
-    float lsum = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int p = 0; p < np; p++) {
-      const size_t part = (size_t)(p < cb.xparts ? cb.xpart0 + p : cb.part0 + p - cb.xparts);
-      const int pr = p < cb.xparts ? cb.xrow + row : row;
-      const float mw = a.part_ml[part * 2 * kAttnRowsP + pr];
-      const float wt = (mw == -INFINITY) ? 0.f : exp2f(mw - mstar);
-      lsum += wt * a.part_ml[part * 2 * kAttnRowsP + kAttnRowsP + pr];
+      const float mp = a.part_ml[part * 2 * kAttnRowsP + pr];
+      const float lp = a.part_ml[part * 2 * kAttnRowsP + kAttnRowsP + pr];
       const float* src = a.part_o + (part * kAttnRowsP + pr) * 128 + d0;
+      const float4_t o0 = *(const float4_t*)src, o1 = *(const float4_t*)(src + 4);
+      const float mn = fmaxf(m, mp);
+      const float sa = (m == -INFINITY) ? 0.f : exp2f(m - mn);
+      const float sb = (mp == -INFINITY) ? 0.f : exp2f(mp - mn);
+      lsum = lsum * sa + sb * lp;
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc[j] += wt * src[j];
+      for (int j = 0; j < 4; j++) {
+        acc[j] = acc[j] * sa + sb * o0[j];
+        acc[4 + j] = acc[4 + j] * sa + sb * o1[j];
+      }
+      m = mn;
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
