@@ -695,10 +695,15 @@ int tgohip_kv_alloc(tgohip_ctx* c, int positions) {
   c->kc = c->vc = nullptr;
   hipError_t e = hipMalloc((void**)&c->kc, n * 2);
   if (e == hipSuccess) e = hipMalloc((void**)&c->vc, n * 2);
-  if (e != hipSuccess)
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (c->kc) (void)hipFree(c->kc);
+    c->kc = c->vc = nullptr;  // no half pool: a step then refuses for want of one
+    c->kv_positions = 0;
     return fail(TGOHIP_ENOMEM, "kv_alloc: the shared prefix cache needs " + std::to_string(n * 2) +
                                    " bytes per state at " + std::to_string(pos) +
                                    " positions and the device refused it");
+  }
   // Zeroed (blocks.go:117-137).
   TGOHIP_HIP(hipMemsetAsync(c->kc, 0, n * 2, c->stream));
   TGOHIP_HIP(hipMemsetAsync(c->vc, 0, n * 2, c->stream));
