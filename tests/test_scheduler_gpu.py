@@ -167,6 +167,8 @@ def run_overlap(sched, steps):
 
 
 def test_overlap_mode_runs_the_synchronous_steps(torch_gpu):
+    """Also twice over, each in a context of its own opened after the last one closed:
+    the second run starts on memory the first released and must not see its state."""
     torch = torch_gpu
     steps = 40
     a, b = new_ctx(torch), new_ctx(torch)
@@ -181,6 +183,14 @@ def test_overlap_mode_runs_the_synchronous_steps(torch_gpu):
     sb.close()
     a.close()
     b.close()
+    for _ in range(2):
+        c = new_ctx(torch)
+        sc = tgo_amd.Scheduler(c, 8, chunk=8, reserve=4, max_rows=64)
+        again, again_sizes = run_overlap(sc, steps)
+        sc.close()
+        c.close()
+        assert again_sizes == sync_sizes
+        assert again == sync_streams
 
 
 def test_overlap_refusals(torch_gpu):
