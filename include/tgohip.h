@@ -126,7 +126,8 @@ int tgohip_synth_weights(tgohip_ctx* ctx, uint64_t seed, int form, double sigma)
 
 /* Allocates the shared KV pool: K and V f16 [layers, positions, kv_heads,
  * head_dim], zeroed (blocks.go:74-139). positions is rounded down to whole
- * pages. */
+ * pages. Any earlier pool is released first; if the device refuses the new
+ * one (TGOHIP_ENOMEM) the context holds no pool until a later call succeeds. */
 int tgohip_kv_alloc(tgohip_ctx* ctx, int positions);
 /* Device pointers of the K and V pools and their capacity in positions. */
 int tgohip_kv_pointers(tgohip_ctx* ctx, void** k, void** v, int* positions);
