@@ -385,8 +385,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X; --gpus %d is not supported (the path "
-              "would shard attention by sequence and the projections by column/row with RCCL, "
-              "see DESIGN.md)" % args.gpus, file=sys.stderr)
+              "would shard attention by sequence and the projections by column/row with RCCL)"
+              % args.gpus, file=sys.stderr)
         sys.exit(2)
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
