@@ -168,6 +168,12 @@ typedef struct {
 int tgohip_step(tgohip_ctx* ctx, const tgohip_batch_step* step, float* logits_out,
                 int32_t* argmax_out, tgohip_timings* timings);
 
+/* The top-two margin of each of the last step's B members, computed on the
+ * device in the argmax pass: TopTwoMargin (internal/conformance/measure.go:91),
+ * the largest logit minus the second largest in float64, 0 for a repeated
+ * maximum. out: host [B] double. Waits for the step. */
+int tgohip_step_margins(tgohip_ctx* ctx, double* out, int B);
+
 /* ---- op-level entry points (isolated configs and unit parity) ----------- */
 
 /* tensor.Attention, ragged + paged + f16 cache (nn/attention.go:234-253;
@@ -189,6 +195,15 @@ int tgohip_paged_attention_replay(tgohip_ctx* ctx, const void* q, int q_dtype, i
                                   const uint32_t* lengths, const uint32_t* extents,
                                   const uint32_t* pages, int max_pages, int block, float scale,
                                   void* out, int out_dtype, int iters);
+
+/* Greedy selection over device logits [B,V] f32: ids[b] (device int32) is the
+ * first index of the strict maximum of row b, the argmax of
+ * sample/stages.go:196-206 (a NaN is never taken after index 0; NaN at index 0
+ * gives 0). margins (device [B] double, or NULL): TopTwoMargin of each row
+ * (internal/conformance/measure.go:91-110), which seeds with x[0], x[1] and
+ * takes later values by strict comparison. V >= 2. */
+int tgohip_greedy(tgohip_ctx* ctx, const float* logits, int B, int V, int32_t* ids,
+                  double* margins);
 
 /* Uploads a weight for tgohip_linear under a handle (any form above). */
 int tgohip_weight_upload(tgohip_ctx* ctx, int form, int K, int N, const void* plane,

@@ -64,6 +64,8 @@ def _load():
         "orc_model_gain": (I, [P, ctypes.c_char_p, P, I]),
         "orc_model_synth": (I, [P, U64, I, D, I]),
         "orc_model_kv": (None, [P, P, P]),
+        "orc_synth_gain": (None, [U64, U64, ctypes.c_size_t, P]),
+        "orc_model_set_fault": (I, [P, I]),
         "orc_model_step": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I]),
         "orc_cpu_ragged_attention": (None, [P, I, I, I, I, P, P, I, P, P, P, I, I, F, P]),
         "orc_cpu_linear": (I, [P, I, I, I, I, P, P, P, P]),
@@ -109,6 +111,18 @@ def synth_normal_f16(seed, stream, n, sigma):
     out = np.empty(n, dtype=np.uint16)
     lib.orc_synth_normal_f16(seed, stream, n, sigma, ptr(out))
     return out
+
+
+def synth_gain(seed, stream, n):
+    """The synthesizer's gains: multiples of 1/8 in [-2, 2)."""
+    out = np.empty(n, dtype=np.float32)
+    lib.orc_synth_gain(seed, stream, n, ptr(out))
+    return out
+
+
+# planted mistakes (orc_model_set_fault), for the sensitivity tests
+FAULT_NONE, FAULT_QKNORM_AFTER_ROPE, FAULT_QK_UNIT_GAIN, FAULT_K_TAKES_Q_GAIN = 0, 1, 2, 3
+FAULT_QK_GAIN_AFTER_ROPE, FAULT_NORM_UNIT_GAIN, FAULT_FINAL_UNIT_GAIN = 4, 5, 6
 
 
 def synth_int4_sym(seed, stream, K, N, sigma):
@@ -208,6 +222,9 @@ class CPUModel:
     def gain(self, port, g):
         g = np.ascontiguousarray(g, dtype=np.float32)
         assert lib.orc_model_gain(self.h, port.encode(), ptr(g), g.size) == 0
+
+    def set_fault(self, fault):
+        assert lib.orc_model_set_fault(self.h, fault) == 0
 
     def kv(self):
         kp, vp = ctypes.c_void_p(), ctypes.c_void_p()

@@ -376,6 +376,110 @@ class Lease:
 
 
 # ---------------------------------------------------------------------------
+# scheduler.go:34-397 + batch.go:235-458 -- Scheduler over a Batch
+# ---------------------------------------------------------------------------
+
+class Scheduler:
+    """tgo.Scheduler (scheduler.go) over a Batch (batch.go) and a prefix Pool, with the
+    forward pass left to `backend(ports, table, max_pages) -> logits [B, V]` (the CPU
+    restatement in the tests). Admit takes the first free slot and leases the prompt plus
+    its reserve (batch.go:235-262, scheduler.go:184-222); step asks nextStep for the
+    work, grows each worker's lease (batchSlot.reserve, batch.go:555-575), packs every
+    slot as a member (batch.go:349-360) with NewBatchStep at exactly the rows the work
+    holds (tgo rounds rows up to a bucket, plan.go:66-77; the padding rows are inert),
+    runs the step, then commits and publishes each worker's blocks (batchSlot.commit,
+    batch.go:577-589) and advances the books (scheduler.go:343-357). The page table is
+    the pool-wide one (batch.go:397-402): pool blocks wide, zero past each lease."""
+
+    def __init__(self, n, chunk, reserve, rows, block, blocks, vocab, heads, kv_heads,
+                 backend):
+        if reserve <= 0:
+            raise Refused("the scheduler's reserve")
+        if n < 2:
+            raise Refused("a batch is two or more")
+        self.chunk = chunk or 512  # DefaultChunk (schedule.go:21)
+        self.reserve, self.rows, self.block = reserve, rows, block
+        self.V, self.H, self.Hkv = vocab, heads, kv_heads
+        self.capacity = blocks * block
+        self.max_pages = blocks
+        self.pool = Pool(block, blocks)
+        self.state = [SchedState() for _ in range(n)]
+        self.lease = [None] * n
+        self.length = [0] * n
+        self.next = 0
+        self.backend = backend
+        self.last = None  # (ports, table) of the last step
+
+    def admit(self, prompt, reserve=0):
+        reserve = reserve or self.reserve
+        free = next((i for i, s in enumerate(self.state) if not s.live), -1)
+        if free < 0:
+            raise Exhausted()
+        self._release(free)
+        lease = self.pool.acquire(list(prompt), reserve=reserve)
+        self.lease[free], self.length[free] = lease, lease.reused
+        self.next += 1
+        self.state[free] = SchedState(True, list(prompt), lease.reused, 0, self.next)
+        return free
+
+    def _release(self, slot):
+        if self.lease[slot] is not None:
+            self.lease[slot].release()
+        self.lease[slot], self.length[slot] = None, 0
+
+    def finish(self, slot):
+        self._release(slot)
+        self.state[slot] = SchedState()
+
+    def evict(self):
+        v = victim(self.state)
+        if v >= 0:
+            self.finish(v)
+        return v
+
+    def feed(self, slot, token):
+        s = self.state[slot]
+        if not s.live or s.prefilled < len(s.prompt):
+            raise Refused("a token fed before the prompt is scored")
+        s.feed = token
+        s.prompt.append(token)
+        s.prefilled += 1
+
+    def step(self):
+        """-> ([(slot, logits row, done)], prefill tokens, decodes)."""
+        work, prefill, decode = next_step(self.state, self.chunk, self.rows)
+        if not work:
+            return [], prefill, decode
+        members = [Member([], self.length[i], list(l.blocks) if l else [])
+                   for i, l in enumerate(self.lease)]
+        for slot, toks in work:
+            lease = self.lease[slot]
+            need = self.length[slot] + len(toks)
+            if need > len(lease.ids):
+                lease.grow(need - len(lease.ids))
+            members[slot] = Member(list(toks), self.length[slot], list(lease.blocks))
+        total = sum(len(t) for _, t in work)
+        ports = new_batch_step(self.V, self.H, self.Hkv, total, members, self.block,
+                               self.capacity)
+        table = page_table([m.pages for m in members], self.max_pages)
+        self.last = (ports, table)
+        logits = self.backend(ports, table, self.max_pages)
+        out = []
+        for slot, toks in work:
+            lease = self.lease[slot]
+            need = self.length[slot] + len(toks)
+            if need > len(lease.ids):
+                lease.commit(list(toks[len(toks) - (need - len(lease.ids)):]))
+            lease.publish(self.length[slot] + len(toks))
+            self.length[slot] += len(toks)
+            st = self.state[slot]
+            if st.prefilled < len(st.prompt):
+                st.prefilled += len(toks)
+            out.append((slot, logits[slot], st.prefilled >= len(st.prompt)))
+        return out, prefill, decode
+
+
+# ---------------------------------------------------------------------------
 # reference test fixtures
 # ---------------------------------------------------------------------------
 
@@ -411,3 +515,21 @@ def argmax_first(row):
         if best is None or v > best:
             best, bi = v, i
     return bi
+
+
+def top_two_margin(row):
+    """TopTwoMargin (internal/conformance/measure.go:91-110): the largest logit minus
+    the second largest, in float64, seeded with row[0], row[1] and folded with strict
+    comparisons. Fewer than two logits is a binding mistake and refused."""
+    if len(row) < 2:
+        raise Refused("TopTwoMargin over fewer than two logits")
+    first, second = float(row[0]), float(row[1])
+    if second > first:
+        first, second = second, first
+    for x in row[2:]:
+        v = float(x)
+        if v > first:
+            first, second = v, first
+        elif v > second:
+            second = v
+    return first - second

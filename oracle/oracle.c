@@ -32,7 +32,14 @@
  *                         plus the C16 probe's page walk.
  *   orc_model_step        pinned: composed of the functions above; checked
  *                         against a float64 referenceForward restatement
- *                         (model/graph_rig_test.go:308-371) on a small model.
+ *                         (model/graph_rig_test.go:308-371) on a small model
+ *                         with f16exact gains, which tells q/k-norm before
+ *                         RoPE from after it (the reference's negative
+ *                         control, graph_rig_test.go:286-351).
+ *   orc_model_set_fault   test-only planted mistakes (gain dropped, gain
+ *                         after RoPE, norm after RoPE, k taking q's gain):
+ *                         the CPU tests show each moves the logits past the
+ *                         bound the GPU step tests apply.
  */
 #include "oracle.h"
 
@@ -633,7 +640,14 @@ struct orc_model {
   float** gains;   /* [L][P_NLAYER] (only gain ports used) */
   uint16_t* kc;    /* [L][C][Hkv][dh] f16 */
   uint16_t* vc;
+  int fault;       /* a planted mistake (ORC_FAULT_*), for the sensitivity tests */
 };
+
+int orc_model_set_fault(orc_model* m, int fault) {
+  if (fault < ORC_FAULT_NONE || fault > ORC_FAULT_FINAL_UNIT_GAIN) return -1;
+  m->fault = fault;
+  return 0;
+}
 
 orc_model* orc_model_new(int layers, int hidden, int heads, int kv_heads, int head_dim, int ffn,
                          int vocab, float eps, float theta, int block, int capacity) {
@@ -731,7 +745,17 @@ int orc_model_gain(orc_model* m, const char* port, const float* g, int width) {
  *   I8:      q = hash%255-127, s = f16(|N|*sigma/64).
  *   I4_TGO:  q = hash&15, s = f16(|N|*sigma/4), z = 7 + (hash&1).
  *   I4_SYM:  q = hash&15 (nibble = q+8 convention), s = f16(|N|*sigma/4).
- * Gains are 1.0. Under int4 the embedding is int8 (weights/weights.go:543-545). */
+ * Gains (stream ids: final_norm 2; a layer's attn_norm, qnorm, knorm, ffn_norm
+ * at (l+1)*64 + 0, 5, 6, 7) are multiples of 1/8 in [-2, 2): g = ((hash%32)-16)/8,
+ * the value set of the reference fixture's f16exact (model/graph_rig_test.go:42-48),
+ * negative and zero gains included, so a dropped, shared-wrongly or misplaced
+ * gain changes the logits. Under int4 the embedding is int8
+ * (weights/weights.go:543-545). */
+void orc_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out) {
+  for (size_t i = 0; i < n; i++)
+    out[i] = (float)((int)(orc_hash3(seed, stream * 4, (uint64_t)i) % 32u) - 16) / 8.0f;
+}
+
 static void synth_weight(orc_weight* w, uint64_t seed, uint64_t stream, int form, int K, int N,
                          double sigma) {
   free_weight(w);
@@ -785,7 +809,7 @@ int orc_model_synth(orc_model* m, uint64_t seed, int form, double sigma, int lay
   synth_weight(&m->lm_head, seed, 3, form, m->d, m->V, sigma);
   free(m->final_norm);
   m->final_norm = (float*)malloc(sizeof(float) * (size_t)m->d);
-  for (int i = 0; i < m->d; i++) m->final_norm[i] = 1.0f;
+  orc_synth_gain(seed, 2, (size_t)m->d, m->final_norm);
   int L = layers_limit < 0 || layers_limit > m->L ? m->L : layers_limit;
   for (int l = 0; l < L; l++) {
     int dims[P_NLAYER][2] = {{0, 0}, {m->d, m->H * m->dh}, {m->d, m->Hkv * m->dh},
@@ -797,7 +821,7 @@ int orc_model_synth(orc_model* m, uint64_t seed, int form, double sigma, int lay
         int w = (p == P_QNORM || p == P_KNORM) ? m->dh : m->d;
         free(m->gains[l * P_NLAYER + p]);
         float* g = (float*)malloc(sizeof(float) * (size_t)w);
-        for (int i = 0; i < w; i++) g[i] = 1.0f;
+        orc_synth_gain(seed, stream, (size_t)w, g);
         m->gains[l * P_NLAYER + p] = g;
       } else {
         synth_weight(&m->lw[l * P_NLAYER + p], seed, stream, form, dims[p][0], dims[p][1], sigma);
@@ -857,6 +881,8 @@ int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uin
   float* y = (float*)malloc(sizeof(float) * (size_t)T * (d > f ? d : f));
   float* gt = (float*)malloc(sizeof(float) * (size_t)T * f);
   float* up = (float*)malloc(sizeof(float) * (size_t)T * f);
+  float* ones = (float*)malloc(sizeof(float) * (size_t)(d > dh ? d : dh));
+  for (int i = 0; i < (d > dh ? d : dh); i++) ones[i] = 1.0f;
   /* rows 3: embedding (model/qwen3_graph.go:54-61) */
   {
     float* row = (float*)malloc(sizeof(float) * (size_t)d);
@@ -871,14 +897,35 @@ int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uin
   for (int l = 0; l < L; l++) {
     orc_weight* W = m->lw + (size_t)l * P_NLAYER;
     float** G = m->gains + (size_t)l * P_NLAYER;
-    cpu_rmsnorm(h, G[P_ATTN_NORM], T, d, m->eps, n);
+    cpu_rmsnorm(h, m->fault == ORC_FAULT_NORM_UNIT_GAIN ? ones : G[P_ATTN_NORM], T, d, m->eps, n);
     cpu_linear_w(n, T, &W[P_WQ], q);
     cpu_linear_w(n, T, &W[P_WK], k);
     cpu_linear_w(n, T, &W[P_WV], v);
-    cpu_rmsnorm(q, G[P_QNORM], T * H, dh, m->eps, q);
-    cpu_rmsnorm(k, G[P_KNORM], T * Hkv, dh, m->eps, k);
-    cpu_rope(q, T * H, dh, (double)m->theta, posq);
-    cpu_rope(k, T * Hkv, dh, (double)m->theta, posk);
+    /* q/k RMSNorm per head with the d_h-wide gain shared by every head, then
+     * RoPE (nn/attention.go:192-211). The planted faults reorder or corrupt
+     * exactly this stage. */
+    const float* gq = G[P_QNORM];
+    const float* gk = G[P_KNORM];
+    if (m->fault == ORC_FAULT_QK_UNIT_GAIN) gq = gk = ones;
+    if (m->fault == ORC_FAULT_K_TAKES_Q_GAIN) gk = gq;
+    if (m->fault == ORC_FAULT_QKNORM_AFTER_ROPE) {
+      cpu_rope(q, T * H, dh, (double)m->theta, posq);
+      cpu_rope(k, T * Hkv, dh, (double)m->theta, posk);
+      cpu_rmsnorm(q, gq, T * H, dh, m->eps, q);
+      cpu_rmsnorm(k, gk, T * Hkv, dh, m->eps, k);
+    } else if (m->fault == ORC_FAULT_QK_GAIN_AFTER_ROPE) {
+      cpu_rmsnorm(q, ones, T * H, dh, m->eps, q);
+      cpu_rmsnorm(k, ones, T * Hkv, dh, m->eps, k);
+      cpu_rope(q, T * H, dh, (double)m->theta, posq);
+      cpu_rope(k, T * Hkv, dh, (double)m->theta, posk);
+      for (size_t i = 0; i < (size_t)T * H * dh; i++) q[i] *= gq[i % (size_t)dh];
+      for (size_t i = 0; i < (size_t)T * Hkv * dh; i++) k[i] *= gk[i % (size_t)dh];
+    } else {
+      cpu_rmsnorm(q, gq, T * H, dh, m->eps, q);
+      cpu_rmsnorm(k, gk, T * Hkv, dh, m->eps, k);
+      cpu_rope(q, T * H, dh, (double)m->theta, posq);
+      cpu_rope(k, T * Hkv, dh, (double)m->theta, posk);
+    }
     /* Cast + ScatterRows, slot >= C dropped (nn/attention.go:225-232; plan.go:182-192) */
     uint16_t* kl = m->kc + (size_t)l * layer_kv;
     uint16_t* vl = m->vc + (size_t)l * layer_kv;
@@ -893,7 +940,7 @@ int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uin
                              m->block, scale, a);
     cpu_linear_w(a, T, &W[P_WO], y);
     for (size_t i = 0; i < (size_t)T * d; i++) h[i] += y[i];
-    cpu_rmsnorm(h, G[P_FFN_NORM], T, d, m->eps, n);
+    cpu_rmsnorm(h, m->fault == ORC_FAULT_NORM_UNIT_GAIN ? ones : G[P_FFN_NORM], T, d, m->eps, n);
     cpu_linear_w(n, T, &W[P_WGATE], gt);
     cpu_linear_w(n, T, &W[P_WUP], up);
     for (size_t i = 0; i < (size_t)T * f; i++) gt[i] = gt[i] / (1.0f + expf(-gt[i])) * up[i];
@@ -903,12 +950,13 @@ int orc_model_step(orc_model* m, int rows, int B, const uint32_t* ids, const uin
   /* rows 26-28: last row per sequence, final norm, head (model/qwen3_graph.go:117-127) */
   float* lastrows = (float*)malloc(sizeof(float) * (size_t)B * d);
   for (int s = 0; s < B; s++) memcpy(lastrows + (size_t)s * d, h + (size_t)last[s] * d, sizeof(float) * (size_t)d);
-  cpu_rmsnorm(lastrows, m->final_norm, B, d, m->eps, lastrows);
+  cpu_rmsnorm(lastrows, m->fault == ORC_FAULT_FINAL_UNIT_GAIN ? ones : m->final_norm, B, d,
+              m->eps, lastrows);
   cpu_linear_w(lastrows, B, &m->lm_head, logits);
   for (int s = 0; s < B; s++)
     if (extents[s] == 0) memset(logits + (size_t)s * V, 0, sizeof(float) * (size_t)V);
   free(lastrows);
-  free(h); free(n); free(q); free(k); free(v); free(a); free(y); free(gt); free(up);
+  free(h); free(n); free(q); free(k); free(v); free(a); free(y); free(gt); free(up); free(ones);
   return 0;
 }
 

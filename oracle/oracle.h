@@ -94,6 +94,19 @@ int  orc_model_gain(orc_model*, const char* port, const float* g, int width);
  * product's synthesizer does; layers_limit < 0 means all layers. */
 int  orc_model_synth(orc_model*, uint64_t seed, int form, double sigma, int layers_limit);
 void orc_model_kv(orc_model*, uint16_t** k, uint16_t** v);
+/* The synthesizer's gains: multiples of 1/8 in [-2, 2) from (seed, stream). */
+void orc_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out);
+/* Planted mistakes for the sensitivity tests (0 = none). */
+enum {
+  ORC_FAULT_NONE = 0,
+  ORC_FAULT_QKNORM_AFTER_ROPE = 1, /* q/k RMSNorm applied after RoPE */
+  ORC_FAULT_QK_UNIT_GAIN = 2,      /* q/k-norm gain dropped */
+  ORC_FAULT_K_TAKES_Q_GAIN = 3,    /* k rows normalized with the q gain */
+  ORC_FAULT_QK_GAIN_AFTER_ROPE = 4,/* normalized, rotated, then scaled by the gain */
+  ORC_FAULT_NORM_UNIT_GAIN = 5,    /* attn_norm / ffn_norm gains dropped */
+  ORC_FAULT_FINAL_UNIT_GAIN = 6    /* final_norm gain dropped */
+};
+int  orc_model_set_fault(orc_model*, int fault);
 /* One batched step: ports as model.NewBatchStep packs them (model/batch.go). Writes
  * logits [B,V] (rows of members with extent 0 are written as zeros). layers < 0: all. */
 int  orc_model_step(orc_model*, int rows, int B, const uint32_t* ids, const uint32_t* posq,

@@ -740,3 +740,43 @@ def test_load_conversions_are_bit_exact_with_the_oracle():
     oracle.lib.orc_quantize_int4_tgo(oracle.ptr(w), w.size, oracle.ptr(oc), oracle.ptr(osc),
                                      oracle.ptr(oz))
     assert np.array_equal(c, oc) and np.array_equal(s, osc) and np.array_equal(z, oz)
+
+
+def test_oracle_scheduler_known_answers():
+    """oracle/host.py's Scheduler against scheduler_test.go:41-113's counts (a dummy forward
+    pass): 6 + 5 prompts under a chunk of 8 are one step of 11 prefill tokens; a 20-token
+    prompt joins two decoders as 8 prefill tokens + 2 decodes and is not sampleable; then
+    8 + 2, 4 + 2 and 3 decodes. Admission takes the first free slot; Admit refuses without
+    one; victim is the last arrival, mid-prefill first."""
+    import numpy as np
+    calls = []
+
+    def backend(st, table, max_pages):
+        calls.append((len(st["ids"]), len(st["lengths"]), max_pages, len(table)))
+        return np.zeros((len(st["lengths"]), 64), np.float32)
+
+    s = host.Scheduler(3, 8, 32, 64, 4, 64, 64, 4, 2, backend)
+    assert s.admit(list(range(1, 7))) == 0 and s.admit(list(range(7, 12))) == 1
+    out, pf, dc = s.step()
+    assert (pf, dc) == (11, 0) and [(o[0], o[2]) for o in out] == [(0, True), (1, True)]
+    assert calls[-1] == (11, 3, 64, 3 * 64)
+    s.feed(0, 5)
+    s.feed(1, 6)
+    assert s.admit(list(range(20, 40))) == 2
+    seen = []
+    for _ in range(4):
+        out, pf, dc = s.step()
+        seen.append((pf, dc, [(o[0], o[2]) for o in out]))
+        for slot, _, done in out:
+            if done:
+                s.feed(slot, 1)
+    assert seen == [(8, 2, [(0, True), (1, True), (2, False)]),
+                    (8, 2, [(0, True), (1, True), (2, False)]),
+                    (4, 2, [(0, True), (1, True), (2, True)]),
+                    (0, 3, [(0, True), (1, True), (2, True)])]
+    with pytest.raises(host.Exhausted):
+        s.admit([1, 2])
+    assert s.evict() == 2  # the last arrival
+    s.finish(0)
+    assert s.admit([1, 2, 3]) == 0
+    assert s.evict() == 0 and s.evict() == 1 and s.evict() == -1

@@ -379,10 +379,15 @@ def test_ragged_oracle_walks_the_page_table():
     assert b["positions"] == 5
 
 
-def reference_forward(cfg, W, ids, f16_cache):
+NORM_BEFORE_ROPE, NORM_AFTER_ROPE = 0, 1  # qkOrder (model/graph_rig_test.go:286-293)
+
+
+def reference_forward(cfg, W, ids, f16_cache, order=NORM_BEFORE_ROPE):
     """model/graph_rig_test.go:308-371 restated: float64 forward of a prefill from an empty
-    cache, composed of the float64 oracle functions, last row's logits. With f16_cache the
-    keys (after norm and RoPE) and values are rounded to f16 as a paged f16 pool stores them."""
+    cache, composed of the float64 oracle functions, last row's logits. Every norm takes
+    its gain from W. With f16_cache the keys (after norm and RoPE) and values are rounded to
+    f16 as a paged f16 pool stores them. order selects q/k-norm before RoPE (Qwen3) or the
+    ordering mistake, after it (graph_rig_test.go:335-347)."""
     t, d, H, Hkv, dh, f, V = len(ids), cfg["d"], cfg["H"], cfg["Hkv"], 128, cfg["f"], cfg["V"]
     eps, base = cfg["eps"], cfg["theta"]
 
@@ -400,59 +405,84 @@ def reference_forward(cfg, W, ids, f16_cache):
     posk = [p for p in range(t) for _ in range(Hkv)]
     h = f64(W["embed"][ids].ravel())
     for l in range(cfg["L"]):
-        n = rms(h, np.ones(d), t, d)
-        q = mm(n, W["%d.wq" % l], t, d, H * dh)
-        k = mm(n, W["%d.wk" % l], t, d, Hkv * dh)
-        v = mm(n, W["%d.wv" % l], t, d, Hkv * dh)
-        q = rope(rms(q, np.ones(dh), t * H, dh), t * H, dh, dh, base, posq, 1)
-        k = rope(rms(k, np.ones(dh), t * Hkv, dh), t * Hkv, dh, dh, base, posk, 1)
+        g = lambda name: W["%d.%s" % (l, name)]
+        n = rms(h, g("attn_norm"), t, d)
+        q = mm(n, g("wq"), t, d, H * dh)
+        k = mm(n, g("wk"), t, d, Hkv * dh)
+        v = mm(n, g("wv"), t, d, Hkv * dh)
+        if order == NORM_BEFORE_ROPE:
+            q = rope(rms(q, g("qnorm"), t * H, dh), t * H, dh, dh, base, posq, 1)
+            k = rope(rms(k, g("knorm"), t * Hkv, dh), t * Hkv, dh, dh, base, posk, 1)
+        else:
+            q = rms(rope(q, t * H, dh, dh, base, posq, 1), g("qnorm"), t * H, dh)
+            k = rms(rope(k, t * Hkv, dh, dh, base, posk, 1), g("knorm"), t * Hkv, dh)
         if f16_cache:
             k = k.astype(np.float16).astype(np.float64)
             v = v.astype(np.float16).astype(np.float64)
         a = attention(q, k, v, t, H, Hkv, dh, t, 1 / math.sqrt(dh), 0)
-        h = h + mm(a, W["%d.wo" % l], t, H * dh, d)
-        n2 = rms(h, np.ones(d), t, d)
-        gt = mm(n2, W["%d.wgate" % l], t, d, f)
-        up = mm(n2, W["%d.wup" % l], t, d, f)
+        h = h + mm(a, g("wo"), t, H * dh, d)
+        n2 = rms(h, g("ffn_norm"), t, d)
+        gt = mm(n2, g("wgate"), t, d, f)
+        up = mm(n2, g("wup"), t, d, f)
         act = np.empty(t * f)
         L.orc_swiglu_f64(P(gt), P(up), t * f, P(act))
-        h = h + mm(act, W["%d.wdown" % l], t, f, d)
-    last = rms(h[(t - 1) * d:], np.ones(d), 1, d)
+        h = h + mm(act, g("wdown"), t, f, d)
+    last = rms(h[(t - 1) * d:], W["final_norm"], 1, d)
     return mm(last, W["lm_head"], 1, d, V)
 
 
 def test_cpu_step_matches_the_float64_reference_forward():
-    """orc_model_step (tgo's f32 CPU path over an f16 paged pool) against referenceForward on
-    f16-exact weights, with the pool's f16 rounding of K and V applied in the reference, to
-    prefillTol (graph_rig_test.go:528-552): 8 * 10 * sqrt(d) * 2^-24 * (2L + 1) on the
-    relative deviation |got - want| / (1 + |want|) (graph_rig_test.go:388-398). Without the
-    rounding the deviation exceeds the budget: the test tells the two caches apart."""
+    """orc_model_step (tgo's f32 CPU path over an f16 paged pool) against referenceForward,
+    to prefillTol (graph_rig_test.go:528-552): 8 * 10 * sqrt(d) * 2^-24 * (2L + 1) on the
+    relative deviation |got - want| / (1 + |want|) (graph_rig_test.go:388-398).
+
+    Every norm gain is a distinct f16exact plane (graph_rig_test.go:42-84: multiples of
+    1/8 in [-2, 2), negatives and zeros included), so a gain dropped, shared wrongly or
+    applied at the wrong place moves the result. Two negative controls show the budget
+    tells things apart: the reference with q/k-norm after RoPE (the ordering mistake,
+    graph_rig_test.go:286-351) and the reference without the pool's f16 rounding of K and
+    V both exceed it."""
     cfg = dict(L=2, d=64, H=4, Hkv=2, f=128, V=96, eps=1e-6, theta=1e6)
     rng = np.random.default_rng(5)
     dh = 128
 
-    def plane(K, N):  # multiples of 1/64 in [-1/4, 1/4): exact in f16 (graph_rig_test.go:42-55)
+    def plane(K, N):  # multiples of 1/64 in [-1/4, 1/4): exact in f16
         return (rng.integers(-16, 16, K * N) / 64.0).astype(np.float32).reshape(K, N)
+
+    ports = []  # f16exact gains, one distinct plane per port (graph_rig_test.go:57-84)
+
+    def gain(name, n):
+        ports.append(name)
+        return np.array([host.f16exact(len(ports) * 7919 + i * 104729 + 1) for i in range(n)],
+                        np.float32)
 
     W = {"embed": plane(cfg["V"], cfg["d"]), "lm_head": plane(cfg["d"], cfg["V"])}
     for l in range(cfg["L"]):
+        W["%d.attn_norm" % l] = gain("%d.attn_norm" % l, cfg["d"])
         W["%d.wq" % l] = plane(cfg["d"], cfg["H"] * dh)
         W["%d.wk" % l] = plane(cfg["d"], cfg["Hkv"] * dh)
         W["%d.wv" % l] = plane(cfg["d"], cfg["Hkv"] * dh)
         W["%d.wo" % l] = plane(cfg["H"] * dh, cfg["d"])
+        W["%d.qnorm" % l] = gain("%d.qnorm" % l, dh)
+        W["%d.knorm" % l] = gain("%d.knorm" % l, dh)
+        W["%d.ffn_norm" % l] = gain("%d.ffn_norm" % l, cfg["d"])
         W["%d.wgate" % l] = plane(cfg["d"], cfg["f"])
         W["%d.wup" % l] = plane(cfg["d"], cfg["f"])
         W["%d.wdown" % l] = plane(cfg["f"], cfg["d"])
+    W["final_norm"] = gain("final_norm", cfg["d"])
+    gains = [n for n in W if n.endswith("norm")]
+    assert len(gains) == 4 * cfg["L"] + 1
+    allg = np.concatenate([W[n] for n in gains])
+    assert (allg < 0).any() and (allg == 0).any() and len(np.unique(allg)) > 20
+    assert not np.array_equal(W["0.qnorm"], W["0.knorm"])
     m = oracle.CPUModel(cfg["L"], cfg["d"], cfg["H"], cfg["Hkv"], dh, cfg["f"], cfg["V"],
                         cfg["eps"], cfg["theta"], 4, 64)
     try:
         for name, w in W.items():
-            m.weight(name, 0, w.shape[0], w.shape[1], oracle.f16_bits(w))
-        for l in range(cfg["L"]):
-            for gname, width in (("attn_norm", cfg["d"]), ("ffn_norm", cfg["d"]), ("qnorm", dh),
-                                 ("knorm", dh)):
-                m.gain("%d.%s" % (l, gname), np.ones(width))
-        m.gain("final_norm", np.ones(cfg["d"]))
+            if name in gains:
+                m.gain(name, w)
+            else:
+                m.weight(name, 0, w.shape[0], w.shape[1], oracle.f16_bits(w))
         ids = [3, 17, 40, 8, 95, 0]
         st = host.new_batch_step(cfg["V"], cfg["H"], cfg["Hkv"], len(ids),
                                  [host.Member(ids, 0, [0, 1]), host.Member([], 0, [2])], 4, 64)
@@ -465,4 +495,77 @@ def test_cpu_step_matches_the_float64_reference_forward():
     want = reference_forward(cfg, W, np.asarray(ids), True)
     assert worst(want) <= tol
     assert int(np.argmax(got)) == int(np.argmax(want))
+    assert worst(reference_forward(cfg, W, np.asarray(ids), True, NORM_AFTER_ROPE)) > 10 * tol
     assert worst(reference_forward(cfg, W, np.asarray(ids), False)) > tol
+
+
+def small_step(cfg):
+    """A prefill chunk of 7 beside a 3-token member and an idle slot, over scattered pages."""
+    rng = np.random.default_rng(12)
+    p0 = [int(t) for t in rng.integers(0, cfg["V"], 7)]
+    p1 = [int(t) for t in rng.integers(0, cfg["V"], 3)]
+    members = [host.Member(p0, 0, [5, 1]), host.Member([], 0, []), host.Member(p1, 0, [9])]
+    st = host.new_batch_step(cfg["V"], cfg["H"], cfg["Hkv"], 10, members, 4, 64)
+    return st, host.page_table([m.pages for m in members], 4)
+
+
+@pytest.mark.parametrize("fault", [oracle.FAULT_QKNORM_AFTER_ROPE, oracle.FAULT_QK_UNIT_GAIN,
+                                   oracle.FAULT_K_TAKES_Q_GAIN, oracle.FAULT_QK_GAIN_AFTER_ROPE,
+                                   oracle.FAULT_NORM_UNIT_GAIN, oracle.FAULT_FINAL_UNIT_GAIN])
+@pytest.mark.parametrize("form", [oracle.FORM_F16, oracle.FORM_I4_SYM])
+def test_planted_mistakes_move_the_logits_past_the_gpu_bound(form, fault):
+    """The GPU step tests hold the device to |gpu - cpu| <= 2e-3 * max|cpu| per row over
+    synthesized models. Planted in the CPU path, each plausible kernel mistake around the
+    norms -- q/k-norm after RoPE, a q/k gain dropped, k normalized with q's gain, the gain
+    applied after the rotation, the attn/ffn gain dropped, the final gain dropped -- moves
+    some row by more than ten times that bound, so none of them could pass those tests."""
+    cfg = dict(L=2, d=256, H=4, Hkv=2, f=512, V=1024, eps=1e-6, theta=1e6)
+    st, pages = small_step(cfg)
+    out = {}
+    for fl in (oracle.FAULT_NONE, fault):
+        m = oracle.CPUModel(cfg["L"], cfg["d"], cfg["H"], cfg["Hkv"], 128, cfg["f"], cfg["V"],
+                            cfg["eps"], cfg["theta"], 4, 64)
+        try:
+            m.synth(11, form, 0.02)
+            m.set_fault(fl)
+            out[fl] = m.step(st, pages, 4)
+        finally:
+            m.close()
+    good, bad = out[oracle.FAULT_NONE], out[fault]
+    assert np.all(good[1] == 0) and np.all(bad[1] == 0)
+    moved = max(np.abs(bad[r] - good[r]).max() / np.abs(good[r]).max() for r in (0, 2))
+    assert moved > 10 * 2e-3, moved
+
+
+def test_synthesized_gains_are_f16exact_valued():
+    """The synthesizer's gains (shared definition with the device): multiples of 1/8 in
+    [-2, 2) -- the value set of f16exact (graph_rig_test.go:42-48) -- with negatives and
+    zeros, distinct per port (stream)."""
+    a = oracle.synth_gain(3, 2, 4096)  # final_norm's stream
+    b = oracle.synth_gain(3, 1 * 64 + 5, 4096)  # layer 0's qnorm
+    for g in (a, b):
+        assert np.all(g * 8 == np.round(g * 8)) and g.min() == -2 and g.max() == 1.875
+        assert (g == 0).any() and (g < 0).mean() > 0.4
+        assert oracle.f16_to_f32(oracle.f16_bits(g)).tolist() == g.tolist()
+    assert not np.array_equal(a, b)
+    want = [((int(L.orc_hash3(3, 2 * 4, i)) % 32) - 16) / 8 for i in range(64)]
+    assert a[:64].tolist() == want
+
+
+def test_top_two_margin_and_argmax_known_answers():
+    """TopTwoMargin (measure_test.go:41-76) and argmax's tie rule (stages_test.go:375)."""
+    for c in GOLD["top_two_margin"]["cases"]:
+        assert abs(host.top_two_margin(np.asarray(c["logits"], np.float32)) - c["want"]) <= 1e-6
+    with pytest.raises(host.Refused, match=GOLD["top_two_margin"]["refuses_one_logit"]):
+        host.top_two_margin([1.0])
+    assert host.argmax_first(GOLD["argmax_ties"]["logits"]) == GOLD["argmax_ties"]["want"]
+    nan, inf = float("nan"), float("inf")
+    # Go's loops by hand: a NaN is never taken after index 0 (argmax) or 1 (margin)
+    assert host.argmax_first([nan, 3, 9]) == 0 and host.argmax_first([1, nan, 9, 9]) == 2
+    assert host.argmax_first([-inf, -inf]) == 0
+    assert math.isnan(host.top_two_margin([nan, 1, 2]))
+    assert math.isnan(host.top_two_margin([5, nan, 3, 4]))  # nothing after displaces x[0]
+    assert host.top_two_margin([5, nan, 3, 6]) == 1.0
+    assert host.top_two_margin([4, 1, nan, 3]) == 1.0
+    assert math.isnan(host.top_two_margin([inf, inf, 1]))
+    assert host.top_two_margin([inf, 3]) == inf

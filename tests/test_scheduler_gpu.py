@@ -249,3 +249,183 @@ def test_profile_times_every_kth_layer(torch_gpu):
     with pytest.raises(tgo_amd.TgoError, match="layer stride"):
         ctx.set_profile(True, -1)
     ctx.close()
+
+
+# ---- the library Scheduler against the reference's, restated ------------------------
+#
+# oracle/host.py's Scheduler restates scheduler.go over Batch.step (batch.go:314-458) and a
+# prefix Pool, with the forward pass on the CPU restatement. The library's Scheduler
+# (tgohip_sched_*, the driver of bench.py) and it are given the same admissions, feeds,
+# finishes and evictions; every step's ports must be equal to the bit (the page table row
+# by row: the library's stride is the step's longest lease, the reference's the pool's) and
+# the greedy tokens equal.
+
+def prompt_ids(seed, n, vocab):
+    """promptIDs (prefixcache_test.go:33-43): a 32-bit xorshift stream over [1, vocab)."""
+    out, x = [], (seed * 2654435761 + 1) & 0xFFFFFFFF
+    for _ in range(n):
+        x ^= (x << 13) & 0xFFFFFFFF
+        x ^= x >> 17
+        x ^= (x << 5) & 0xFFFFFFFF
+        out.append(1 + x % (vocab - 1))
+    return out
+
+
+class Pair:
+    """The library Scheduler on the GPU and the oracle Scheduler on the CPU path."""
+
+    def __init__(self, torch, n, chunk, reserve, max_rows, form=3, seed=21):
+        import oracle
+        c = CFG
+        self.ctx = new_ctx(torch, form, seed)
+        self.lib = tgo_amd.Scheduler(self.ctx, n, chunk=chunk, reserve=reserve,
+                                     max_rows=max_rows)
+        self.cpu = oracle.CPUModel(c["layers"], c["hidden"], c["heads"], c["kv_heads"],
+                                   c["head_dim"], c["ffn"], c["vocab"], c["eps"], c["theta"],
+                                   c["block"], c["positions"])
+        self.cpu.synth(seed, form, 0.02)
+        self.orc = host.Scheduler(n, chunk, reserve, max_rows, c["block"],
+                                  c["positions"] // c["block"], c["vocab"], c["heads"],
+                                  c["kv_heads"], lambda st, tb, mp: self.cpu.step(st, tb, mp))
+        self.near = 0
+
+    def close(self):
+        self.lib.close()
+        self.ctx.close()
+        self.cpu.close()
+
+    def admit(self, prompt, reserve=0):
+        a = self.lib.admit(prompt, reserve)
+        b = self.orc.admit(prompt, reserve)
+        assert a == b, ("admit took different slots", a, b)
+        assert self.lib.length(a) == self.orc.length[a]  # the prefix pool's reuse
+        return a
+
+    def finish(self, slot):
+        self.lib.finish(slot)
+        self.orc.finish(slot)
+
+    def evict(self):
+        a, b = self.lib.evict(), self.orc.evict()
+        assert a == b
+        return a
+
+    def step(self):
+        """One step on both; checks the ports, the books and the tokens and feeds the
+        tokens. -> ([(slot, token, done)], prefill, decodes)."""
+        got, pf, dc, _ = self.lib.step()
+        want, pf2, dc2 = self.orc.step()
+        assert (pf, dc) == (pf2, dc2)
+        assert [(s, d) for s, _, d in got] == [(s, d) for s, _, d in want]
+        if not got:
+            return [], pf, dc
+        st, pages, maxp = self.lib.last_step()
+        ost, otable = self.orc.last
+        for k in ("ids", "posq", "posk", "slots", "lengths", "extents", "last"):
+            assert np.array_equal(np.asarray(st[k], np.uint32), np.asarray(ost[k], np.uint32)), k
+        B, omax = len(ost["lengths"]), self.orc.max_pages
+        lt = np.asarray(pages, np.uint32).reshape(B, maxp)
+        ot = np.asarray(otable, np.uint32).reshape(B, omax)
+        assert np.array_equal(lt, ot[:, :maxp]) and not ot[:, maxp:].any()
+        out = []
+        for (slot, tok, done), (_, logits, _) in zip(got, want):
+            if done:
+                cpu_tok = int(np.argmax(logits))
+                if tok != cpu_tok:  # only a near tie may flip
+                    top = np.sort(logits.astype(np.float64))[-2:]
+                    assert top[1] - top[0] <= 1e-3 * np.abs(logits).max(), (slot, tok, cpu_tok)
+                    self.near += 1
+                self.lib.feed(slot, cpu_tok)
+                self.orc.feed(slot, cpu_tok)
+                tok = cpu_tok
+            out.append((slot, tok, done))
+        return out, pf, dc
+
+
+def test_a_chunk_and_the_decodes_run_in_one_dispatch(torch_gpu):
+    """scheduler_test.go:41-113 on the library Scheduler, checked step by step against the
+    reference's Scheduler restated: prompts of 6 and 5 are one step of 11 prefill tokens
+    (the chunk of 8 is per sequence); a 20-token prompt admitted beside the two decoders is
+    chunked in the same dispatch (8 prefill tokens + 2 decodes) and is not sampleable."""
+    V = CFG["vocab"]
+    p = Pair(torch_gpu, 3, 8, 32, 64)
+    try:
+        for i, prompt in enumerate((prompt_ids(2, 6, V), prompt_ids(3, 5, V))):
+            assert p.admit(prompt) == i
+        out, pf, dc = p.step()
+        assert (pf, dc) == (11, 0) and all(d for _, _, d in out)
+        slot = p.admit(prompt_ids(1, 20, V))
+        out, pf, dc = p.step()
+        assert (pf, dc) == (8, 2) and len(out) == 3
+        assert [d for s, _, d in out if s == slot] == [False]
+        for _ in range(3):  # the long prompt finishes: 8 + 4, then decodes
+            out, pf, dc = p.step()
+        assert (pf, dc) == (0, 3)
+    finally:
+        p.close()
+
+
+def test_a_schedulers_decodes_match_the_sessions_they_batch(torch_gpu):
+    """scheduler_test.go:115-190: two prompts (6 and 10 tokens, chunk 8) stepped together
+    for six steps, feeding greedy tokens, generate what each generates alone."""
+    V = CFG["vocab"]
+    prompts = [prompt_ids(4, 6, V), prompt_ids(5, 10, V)]
+
+    def run(which):
+        p = Pair(torch_gpu, 2, 8, 32, 64)
+        try:
+            for i in which:
+                p.admit(prompts[i])
+            made = {i: [] for i in which}
+            slot_of = {s: i for s, i in enumerate(which)}
+            for _ in range(6):
+                out, _, _ = p.step()
+                for s, tok, done in out:
+                    if done:
+                        made[slot_of[s]].append(tok)
+            return made
+        finally:
+            p.close()
+
+    together = run([0, 1])
+    for i in (0, 1):
+        alone = run([i])[i]
+        assert together[i] and together[i][:len(alone)] == alone[:len(together[i])], i
+
+
+def test_the_library_scheduler_runs_the_reference_schedulers_steps(torch_gpu):
+    """A seeded walk of 60 steps: admissions (prompts that share an 8-token prefix, so the
+    pool reuses published blocks), feeds, finishes and evictions, the same on both sides;
+    every step's ports bit-exact and every greedy token equal."""
+    V = CFG["vocab"]
+    rng = np.random.default_rng(17)
+    p = Pair(torch_gpu, 6, 8, 4, 40)
+    common = prompt_ids(9, 8, V)
+    made = {}
+    try:
+        steps = 0
+        for it in range(60):
+            live = [s for s in range(6) if p.orc.state[s].live]
+            if len(live) < 6 and rng.random() < 0.5:
+                n = int(rng.integers(3, 24))
+                prompt = (common if rng.random() < 0.5 else []) + \
+                    [int(t) for t in rng.integers(0, V, n)]
+                s = p.admit(prompt, reserve=int(rng.integers(4, 16)))
+                made[s] = 0
+            decoding = [s for s in live if p.orc.state[s].prefilled >= len(p.orc.state[s].prompt)]
+            if decoding and rng.random() < 0.2:
+                s = int(rng.choice(decoding))
+                p.finish(s)
+            if live and rng.random() < 0.05:
+                p.evict()
+            out, _, _ = p.step()
+            steps += bool(out)
+            for s, _, done in out:
+                if done:
+                    made[s] = made.get(s, 0) + 1
+                    if made[s] >= 12:  # the reserve is spent: retire it
+                        p.finish(s)
+        assert steps >= 40 and p.near <= 1
+        assert p.orc.pool.stats["hits"] > 0 and p.orc.pool.stats["reused"] > 0
+    finally:
+        p.close()

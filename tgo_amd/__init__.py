@@ -84,6 +84,8 @@ def lib():
         "tgohip_linear": (I, [P, I, P, I, I, P, I]),
         "tgohip_dequant": (I, [P, I, P]),
         "tgohip_dequant_f16": (I, [P, I, P]),
+        "tgohip_greedy": (I, [P, P, I, I, P, P]),
+        "tgohip_step_margins": (I, [P, P, I]),
         "tgohip_new_batch_step": (I, [I, I, I, I, I, P, P, P, P, P, I, I, I, P, P, P, P, P, P, P]),
         "tgohip_next_step": (I, [I, P, P, P, I, I, P, P, P, P, P, P]),
         "tgohip_victim": (I, [I, P, P, P, P]),
@@ -543,6 +545,16 @@ class Context:
 
     def linear(self, handle, x, M, y, x_dtype=F32, y_dtype=F32):
         check(lib().tgohip_linear(self.h, handle, ptr(x), x_dtype, M, ptr(y), y_dtype))
+
+    def greedy(self, logits, B, V, ids, margins=None):
+        """sample argmax (first strict maximum) and TopTwoMargin over device rows."""
+        check(lib().tgohip_greedy(self.h, ptr(logits), B, V, ptr(ids), ptr(margins)))
+
+    def step_margins(self, B):
+        """TopTwoMargin of each member of the last step (float64, host)."""
+        out = np.zeros(B, np.float64)
+        check(lib().tgohip_step_margins(self.h, ptr(out), B))
+        return out
 
     def dequant(self, handle, y):
         check(lib().tgohip_dequant(self.h, handle, ptr(y)))

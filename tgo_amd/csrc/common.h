@@ -171,9 +171,11 @@ struct DeriveArgs {
   uint32_t* slot;  // [T]
 };
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st);
-// keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1).
+// keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1);
+// extents == null: every row is live. margin (nullable): the row's top-two
+// margin in float64 (TopTwoMargin).
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st, int keep_idle = 0);
+                   hipStream_t st, int keep_idle = 0, double* margin = nullptr);
 void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st);
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st);
@@ -183,6 +185,7 @@ void launch_synth_i4sym(uint64_t seed, uint64_t stream, int K, int N, uint32_t* 
 void launch_synth_i4tgo(uint64_t seed, uint64_t stream, size_t n, uint32_t* out, hipStream_t st);
 void launch_synth_zero(uint64_t seed, uint64_t stream, size_t n, uint16_t* out, hipStream_t st);
 void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipStream_t st);
+void launch_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out, hipStream_t st);
 void launch_fill_f32(float* p, size_t n, float v, hipStream_t st);
 
 }  // namespace tgohip

@@ -200,60 +200,87 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
 // or nothing exceeds it. One 1024-thread block per row; each thread scans its
 // 16-byte chunks in increasing index order, then the block reduces (larger
 // value, or equal value at a smaller index).
+//
+// With margin != null the same pass gives TopTwoMargin
+// (internal/conformance/measure.go:91-110): the largest logit minus the
+// second largest, counting a repeated maximum twice (margin 0), in float64.
+// Go seeds (first, second) with x[0], x[1] and folds the rest with strict
+// comparisons, so a NaN after index 1 is never taken; the order-free
+// reduction here keeps the top two of the non-NaN values and restates Go's
+// two seeded cases: x[0] NaN gives NaN, and x[1] NaN gives NaN unless a later
+// value exceeds x[0] (exactly when the argmax is not 0).
+// extents == null treats every row as live.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V,
                                                       const uint32_t* extents, int32_t* out,
-                                                      int keep_idle) {
-  __shared__ float sv[16];
+                                                      int keep_idle, double* margin) {
+  __shared__ float sv[16], s1[16], s2[16];
   __shared__ int si[16];
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float* row = logits + (size_t)b * V;
-  float best = -INFINITY;
+  float best = -INFINITY, t1 = -INFINITY, t2 = -INFINITY;
   int bi = 0x7fffffff;
+  auto take = [&](float v, int i) {
+    if (v > best) {
+      best = v;
+      bi = i;
+    }
+    if (v > t1) {
+      t2 = t1;
+      t1 = v;
+    } else if (v > t2) {
+      t2 = v;
+    }
+  };
   const int V4 = V / 4;
   const float4_t* row4 = (const float4_t*)row;  // rows are 16-byte aligned when V % 4 == 0
   if ((V & 3) == 0) {
     for (int i4 = t; i4 < V4; i4 += 1024) {
       const float4_t v = row4[i4];
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (v[j] > best) {
-          best = v[j];
-          bi = 4 * i4 + j;
-        }
+      for (int j = 0; j < 4; j++) take(v[j], 4 * i4 + j);
     }
   } else {
-    for (int i = t; i < V; i += 1024)
-      if (row[i] > best) {
-        best = row[i];
-        bi = i;
-      }
+    for (int i = t; i < V; i += 1024) take(row[i], i);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float v2 = __shfl_xor(best, o, 64);
-    const int i2 = __shfl_xor(bi, o, 64);
+  // merge two (top1, top2) pairs: top1 = max, top2 = max(min(top1s), max(top2s))
+  auto merge = [&](float v2, int i2, float a1, float a2) {
     if (v2 > best || (v2 == best && i2 < bi)) {
       best = v2;
       bi = i2;
     }
+    const float lo = fminf(t1, a1), hi2 = fmaxf(t2, a2);
+    t1 = fmaxf(t1, a1);
+    t2 = fmaxf(lo, hi2);
+  };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(best, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    const float a1 = __shfl_xor(t1, o, 64), a2 = __shfl_xor(t2, o, 64);
+    merge(v2, i2, a1, a2);
   }
   if (lane == 0) {
     sv[wave] = best;
     si[wave] = bi;
+    s1[wave] = t1;
+    s2[wave] = t2;
   }
   __syncthreads();
   if (t == 0) {
-    for (int w = 1; w < 16; w++)
-      if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-        best = sv[w];
-        bi = si[w];
-      }
+    for (int w = 1; w < 16; w++) merge(sv[w], si[w], s1[w], s2[w]);
     // x[0] itself, and NaN at x[0], are Go's starting point
     const float x0 = row[0];
     int r = bi;
     if (x0 != x0 || bi == 0x7fffffff || !(best > x0)) r = 0;
-    if (extents[b] != 0) out[b] = r;
+    const bool live = !extents || extents[b] != 0;
+    if (live) out[b] = r;
     else if (!keep_idle) out[b] = -1;
+    if (margin) {
+      const float x1 = row[1];
+      double mg = (double)t1 - (double)t2;
+      if (x0 != x0 || (x1 != x1 && r == 0)) mg = __builtin_nan("");
+      margin[b] = mg;
+    }
   }
 }
 
@@ -351,6 +378,12 @@ __global__ void synth_i8_kernel(uint64_t seed, uint64_t stream, size_t n, int8_t
   if (i >= n) return;
   out[i] = (int8_t)((int)(hash3(seed, stream, i) % 255u) - 127);
 }
+// Norm gains: multiples of 1/8 in [-2, 2), ((hash % 32) - 16) / 8.
+__global__ void synth_gain_kernel(uint64_t seed, uint64_t stream, size_t n, float* out) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (float)((int)(hash3(seed, stream, i) % 32u) - 16) / 8.0f;
+}
 __global__ void fill_f32_kernel(float* p, size_t n, float v) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -380,8 +413,9 @@ void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);
 }
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st, int keep_idle) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out, keep_idle);
+                   hipStream_t st, int keep_idle, double* margin) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out, keep_idle,
+                     margin);
 }
 void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st) {
   hipLaunchKernelGGL(zero_idle_rows_kernel, dim3(B), dim3(256), 0, st, logits, V, extents);
@@ -405,6 +439,9 @@ void launch_synth_zero(uint64_t seed, uint64_t stream, size_t n, uint16_t* out, 
 }
 void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipStream_t st) {
   hipLaunchKernelGGL(synth_i8_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, out);
+}
+void launch_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(synth_gain_kernel, grid1(n), dim3(256), 0, st, seed, stream, n, out);
 }
 void launch_fill_f32(float* p, size_t n, float v, hipStream_t st) {
   hipLaunchKernelGGL(fill_f32_kernel, grid1(n), dim3(256), 0, st, p, n, v);

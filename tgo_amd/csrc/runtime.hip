@@ -63,8 +63,12 @@ struct DevBuf {
   }
 };
 
+// Sub-ports of a layer's fused projections, one bit each once uploaded.
+enum { SUB_WQ = 1, SUB_WK = 2, SUB_WV = 4, SUB_WGATE = 8, SUB_WUP = 16, SUB_ALL = 31 };
+
 struct Layer {
   PackedWeight qkv, wo, gateup, down;
+  int bound = 0;  // SUB_* bits of the fused QKV and gate/up sub-ports written
   float* g_attn = nullptr;
   float* g_ffn = nullptr;
   float* g_q = nullptr;
@@ -95,7 +99,7 @@ struct tgohip_ctx {
   int precision = 0;  // 0: f16 activations into MFMA, 1: f32 activations (hi+lo)
   int cascade = 0;    // minimum sequences sharing a prefix for prefix-shared attention (0: off)
   // activations and workspaces
-  DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, meta, gemm_ws, part_o, part_ml;
+  DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, margin, meta, gemm_ws, part_o, part_ml;
   DevBuf rows;  // [2][rows]: positions and slots derived on the device
   int rows_cap = 0, batch_cap = 0;
   // pinned staging for per-step metadata
@@ -207,23 +211,25 @@ size_t plane_bytes(int form, int K, int N) {
 }
 
 // Allocates w as a packed [K, N] weight of `form`.
+// Allocates w as a packed [K, N] weight of `form`. The weight counts as bound
+// (form >= 0) only once every buffer is allocated; a failure frees the ones
+// that were and leaves w unbound.
 int alloc_packed(tgohip_ctx* c, PackedWeight& w, int form, int K, int N) {
-  w.form = form;
-  w.K = K;
-  w.N = N;
-  int rc = alloc_owned(c, &w.wp, packed_payload_bytes(form, K, N));
-  if (rc) return rc;
+  PackedWeight n;
+  int rc = alloc_owned(c, &n.wp, packed_payload_bytes(form, K, N));
   const size_t sh = packed_scale_halves(form, K, N);
-  w.ws = nullptr;
-  w.wz = nullptr;
-  if (sh) {
-    rc = alloc_owned(c, (void**)&w.ws, sh * 2);
-    if (rc) return rc;
+  if (!rc && sh) rc = alloc_owned(c, (void**)&n.ws, sh * 2);
+  if (!rc && form == TGOHIP_FORM_I4_TGO) rc = alloc_owned(c, (void**)&n.wz, sh * 2);
+  if (rc) {
+    free_owned(c, n.wp);
+    free_owned(c, n.ws);
+    free_owned(c, n.wz);
+    return rc;
   }
-  if (form == TGOHIP_FORM_I4_TGO) {
-    rc = alloc_owned(c, (void**)&w.wz, sh * 2);
-    if (rc) return rc;
-  }
+  n.form = form;
+  n.K = K;
+  n.N = N;
+  w = n;
   return 0;
 }
 
@@ -367,8 +373,21 @@ int place_weight(tgohip_ctx* c, PortKind kind, int l, int form, int K, int N, co
   if (w->form < 0) {
     rc = alloc_packed(c, *w, form, K, fusedN);
     if (rc) return rc;
+    // a fresh fused buffer holds none of its sub-ports yet
+    if (kind == P_WQ || kind == P_WK || kind == P_WV) c->layers[l].bound &= ~(SUB_WQ | SUB_WK | SUB_WV);
+    if (kind == P_WGATE || kind == P_WUP) c->layers[l].bound &= ~(SUB_WGATE | SUB_WUP);
   }
-  return repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, *w, stride, off, c->stream);
+  rc = repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, *w, stride, off, c->stream);
+  if (rc) return rc;
+  switch (kind) {
+    case P_WQ: c->layers[l].bound |= SUB_WQ; break;
+    case P_WK: c->layers[l].bound |= SUB_WK; break;
+    case P_WV: c->layers[l].bound |= SUB_WV; break;
+    case P_WGATE: c->layers[l].bound |= SUB_WGATE; break;
+    case P_WUP: c->layers[l].bound |= SUB_WUP; break;
+    default: break;
+  }
+  return 0;
 }
 
 int ensure_activations(tgohip_ctx* c, int rows, int B) {
@@ -391,6 +410,7 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
     if ((rc = c->lastn.ensure((size_t)B * d * 4))) return rc;
     if ((rc = c->logits.ensure((size_t)B * m.vocab * 4))) return rc;
     if ((rc = c->argmax.ensure((size_t)B * 4))) return rc;
+    if ((rc = c->margin.ensure((size_t)B * 8))) return rc;
     c->batch_cap = B;
   }
   // split-K workspace: the largest any projection of this step may ask for
@@ -465,7 +485,8 @@ void tgohip_close(tgohip_ctx* c) {
   for (void* p : c->allocs) (void)hipFree(p);
   c->allocs.clear();
   for (DevBuf* b : {&c->h, &c->xn, &c->qkv, &c->q, &c->attn, &c->act, &c->lastn, &c->logits,
-                    &c->argmax, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml})
+                    &c->argmax, &c->margin, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml,
+                    &c->rows})
     b->release();
   if (c->kc) (void)hipFree(c->kc);
   if (c->vc) (void)hipFree(c->vc);
@@ -648,23 +669,27 @@ int tgohip_synth_weights(tgohip_ctx* c, uint64_t seed, int form, double sigma) {
     if ((rc = place_weight(c, P_LMHEAD, -1, form, d, m.vocab, cn, "lm_head"))) return rc;
     TGOHIP_HIP(hipStreamSynchronize(c->stream));
   }
-  auto ones = [&](float** dst, int w) -> int {
+  // Gains: multiples of 1/8 in [-2, 2) from (seed, port stream), the CPU
+  // restatement's orc_synth_gain (final_norm is stream 2, a layer's gains
+  // streams (l+1)*64 + 0, 5, 6, 7).
+  auto gain = [&](float** dst, int w, uint64_t stream) -> int {
     if (!*dst) {
       int r = alloc_owned(c, (void**)dst, (size_t)w * 4);
       if (r) return r;
     }
-    launch_fill_f32(*dst, (size_t)w, 1.0f, c->stream);
+    launch_synth_gain(seed, stream * 4, (size_t)w, *dst, c->stream);
     return 0;
   };
-  if ((rc = ones(&c->g_final, d))) return rc;
+  if ((rc = gain(&c->g_final, d, 2))) return rc;
   struct P { PortKind k; int p; int K, N; const char* name; };
   const P ports[] = {{P_WQ, 1, d, qw, "wq"}, {P_WK, 2, d, kw, "wk"}, {P_WV, 3, d, kw, "wv"},
                      {P_WO, 4, qw, d, "wo"}, {P_WGATE, 8, d, f, "wgate"}, {P_WUP, 9, d, f, "wup"},
                      {P_WDOWN, 10, f, d, "wdown"}};
   for (int l = 0; l < m.layers; l++) {
     Layer& L = c->layers[l];
-    if ((rc = ones(&L.g_attn, d)) || (rc = ones(&L.g_ffn, d)) || (rc = ones(&L.g_q, kHeadDim)) ||
-        (rc = ones(&L.g_k, kHeadDim)))
+    const uint64_t ls = (uint64_t)(l + 1) * 64;
+    if ((rc = gain(&L.g_attn, d, ls + 0)) || (rc = gain(&L.g_ffn, d, ls + 7)) ||
+        (rc = gain(&L.g_q, kHeadDim, ls + 5)) || (rc = gain(&L.g_k, kHeadDim, ls + 6)))
       return rc;
     for (const P& p : ports) {
       Canon cn;
@@ -743,8 +768,13 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     return fail(TGOHIP_ESTATE, "step: the embedding, lm_head and final_norm are bound first");
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
-    if (L.qkv.form < 0 || L.wo.form < 0 || L.gateup.form < 0 || L.down.form < 0 || !L.g_attn ||
-        !L.g_ffn || !L.g_q || !L.g_k)
+    static const std::pair<int, const char*> subs[] = {
+        {SUB_WQ, "wq"}, {SUB_WK, "wk"}, {SUB_WV, "wv"}, {SUB_WGATE, "wgate"}, {SUB_WUP, "wup"}};
+    for (const auto& sp : subs)
+      if (!(L.bound & sp.first))
+        return fail(TGOHIP_ESTATE, "step: layer " + std::to_string(l) + " has an unbound port (" +
+                                       std::to_string(l) + "." + sp.second + ")");
+    if (L.wo.form < 0 || L.down.form < 0 || !L.g_attn || !L.g_ffn || !L.g_q || !L.g_k)
       return fail(TGOHIP_ESTATE, "step: layer " + std::to_string(l) + " has an unbound port");
   }
   const int T = s->rows, B = s->batch;
@@ -883,7 +913,8 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
   launch_zero_idle((float*)c->logits.p, B, m.vocab, d_ext, st);
-  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st, o.keep_idle);
+  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st, o.keep_idle,
+                (double*)c->margin.p);
   TGOHIP_HIP(hipEventRecord(o.ev_end, st));
   TGOHIP_HIP(hipGetLastError());
   return 0;
@@ -936,7 +967,33 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   return 0;
 }
 
+// The top-two margins of the last step's members (TopTwoMargin,
+// internal/conformance/measure.go:91), waiting for the step to land.
+int tgohip_step_margins(tgohip_ctx* c, double* out, int B) {
+  if (B <= 0 || B > c->batch_cap || !c->margin.p)
+    return fail(TGOHIP_EINVAL, "step margins: " + std::to_string(B) + " members asked and the last "
+                               "step held at most " + std::to_string(c->batch_cap));
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  TGOHIP_HIP(hipMemcpy(out, c->margin.p, (size_t)B * 8, hipMemcpyDeviceToHost));
+  return 0;
+}
+
 // ---- op level ---------------------------------------------------------------
+// Greedy selection over B rows of V logits in device memory
+// (sample/stages.go:196-206 argmax; TopTwoMargin of
+// internal/conformance/measure.go:91 when margins is not null).
+int tgohip_greedy(tgohip_ctx* c, const float* logits, int B, int V, int32_t* ids, double* margins) {
+  if (B < 0) return fail(TGOHIP_EINVAL, "greedy: " + std::to_string(B) + " rows");
+  if (V < 2)
+    return fail(TGOHIP_EINVAL, "greedy: a vocabulary of " + std::to_string(V) +
+                                   " logits; the top-two margin is over at least two");
+  if (B == 0) return 0;
+  if (!logits || !ids) return fail(TGOHIP_EINVAL, "greedy: logits and ids are device buffers");
+  launch_argmax(logits, B, V, nullptr, ids, c->stream, 0, margins);
+  TGOHIP_HIP(hipGetLastError());
+  return 0;
+}
+
 int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int H, int H_kv,
                            int head_dim, const void* k, const void* v, int capacity, int B,
                            const uint32_t* lengths, const uint32_t* extents, const uint32_t* pages,
