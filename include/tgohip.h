@@ -219,6 +219,18 @@ int tgohip_weight_free(tgohip_ctx* ctx, int handle);
 int tgohip_linear(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M, void* y,
                   int y_dtype);
 
+/* tgohip_linear without allocating device memory. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The caller
+ * passes x and y; the split-K partials go to a static 64 MiB device array (one
+ * per GPU, held until the process ends) instead of the context's workspace.
+ * Same kernels and splits as tgohip_linear, so the same result. A call whose
+ * partials need more than 64 MiB is refused (TGOHIP_EINVAL). Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams or
+ * two contexts at once) race; calls in stream order do not. */
+int tgohip_linear_noalloc(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M,
+                          void* y, int y_dtype);
+
 /* Dequantizes a handle's weight to f32 [K,N] on the device exactly as the
  * host restatement does ((q - z) * s in f32). y: device [K,N] f32. */
 int tgohip_dequant(tgohip_ctx* ctx, int handle, float* y);

@@ -1,0 +1,59 @@
+"""tgohip_linear_noalloc -- the linear whose split-K partials live in the library's
+static device workspace -- against tgohip_linear, through the C ABI: the same kernels and
+splits, so the outputs are equal to the bit. Two calls in a row, the second with fewer
+rows, so the second runs on the array the first left behind; shapes where split-K runs
+(the workspace is used) and where it does not; a call needing more than the array holds is
+refused."""
+import numpy as np
+import pytest
+
+import oracle
+import tgo_amd
+
+pytestmark = pytest.mark.gpu
+
+
+def weight(ctx, form, K, N, seed):
+    return ctx.weight_synth(form, K, N, seed, 7, 0.02)
+
+
+@pytest.mark.parametrize("form,K,N,Ms,xf", [
+    (tgo_amd.FORM_I4_SYM, 12288, 4096, (256, 1), tgo_amd.F16),   # pipe kernel 8 splits, then gemm_kernel 32
+    (tgo_amd.FORM_I4_SYM, 12288, 4096, (1024, 512), tgo_amd.F16),  # 4 then 8 splits, 64 MiB each
+    (tgo_amd.FORM_I8, 4096, 6144, (64, 8), tgo_amd.F16),
+    (tgo_amd.FORM_F16, 4096, 4096, (200, 33), tgo_amd.F32),       # gemm_kernel, 16 splits, f32 x
+    (tgo_amd.FORM_I4_TGO, 4096, 12288, (130, 1), tgo_amd.F16),
+])
+def test_noalloc_linear_equals_linear(ctx, torch_gpu, form, K, N, Ms, xf):
+    torch = torch_gpu
+    h = weight(ctx, form, K, N, 3 + form)
+    try:
+        for M in Ms:
+            print("no-alloc linear: form %d [%d,%d] M=%d" % (form, K, N, M), flush=True)
+            g = torch.Generator(device="cuda").manual_seed(M)
+            x = torch.randn(M, K, device="cuda", generator=g)
+            x = x.half() if xf == tgo_amd.F16 else x
+            want = torch.full((M, N), float("nan"), device="cuda")
+            got = torch.full((M, N), float("nan"), device="cuda")
+            ctx.linear(h, x, M, want, x_dtype=xf)
+            ctx.linear_noalloc(h, x, M, got, x_dtype=xf)
+            torch.cuda.synchronize()
+            assert torch.isfinite(want).all()
+            assert torch.equal(got, want), (M, (got - want).abs().max().item())
+    finally:
+        ctx.weight_free(h)
+
+
+def test_noalloc_linear_refuses_beyond_its_workspace(ctx, torch_gpu):
+    """f32 activations over [12288, 4096] at M = 2100: two partial planes of 34 MiB."""
+    torch = torch_gpu
+    h = weight(ctx, tgo_amd.FORM_F16, 12288, 4096, 5)
+    try:
+        x = torch.zeros(2100, 12288, device="cuda")
+        y = torch.zeros(2100, 4096, device="cuda")
+        with pytest.raises(tgo_amd.TgoError, match="static workspace holds 67108864"):
+            ctx.linear_noalloc(h, x, 2100, y)
+        ctx.linear_noalloc(h, x, 2000, y)  # two planes of 32 MiB fit
+        torch.cuda.synchronize()
+    finally:
+        ctx.weight_free(h)

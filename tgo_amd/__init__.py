@@ -82,6 +82,7 @@ def lib():
         "tgohip_weight_synth": (I, [P, I, I, I, U64, U64, D, P]),
         "tgohip_weight_free": (I, [P, I]),
         "tgohip_linear": (I, [P, I, P, I, I, P, I]),
+        "tgohip_linear_noalloc": (I, [P, I, P, I, I, P, I]),
         "tgohip_dequant": (I, [P, I, P]),
         "tgohip_dequant_f16": (I, [P, I, P]),
         "tgohip_greedy": (I, [P, P, I, I, P, P]),
@@ -555,6 +556,10 @@ class Context:
         out = np.zeros(B, np.float64)
         check(lib().tgohip_step_margins(self.h, ptr(out), B))
         return out
+
+    def linear_noalloc(self, handle, x, M, y, x_dtype=F32, y_dtype=F32):
+        """linear with its split-K partials in the library's static workspace."""
+        check(lib().tgohip_linear_noalloc(self.h, handle, ptr(x), x_dtype, M, ptr(y), y_dtype))
 
     def dequant(self, handle, y):
         check(lib().tgohip_dequant(self.h, handle, ptr(y)))

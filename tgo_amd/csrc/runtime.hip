@@ -11,6 +11,7 @@
 #include <deque>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -29,6 +30,33 @@ std::string hip_message(hipError_t e, const char* what) {
 }
 
 constexpr size_t kBufAlign = (size_t)2 << 20;
+
+// The allocation-free linear's split-K workspace: a static device array, one
+// copy per GPU the library runs on, held until the process ends. Host code
+// never passes `scratch` itself (its host-side name is not a device address):
+// tgohip_open looks up each device's address once with hipGetSymbolAddress
+// and every launch takes that address.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// With `device` current: its address of `scratch`, looked up on first use.
+int scratch_setup(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(TGOHIP_EDEVICE, "scratch: device " + std::to_string(device) + " beyond the table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TGOHIP_EDEVICE, hip_message(e, "hipGetSymbolAddress(scratch)"));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return 0;
+}
 
 // Grow-only device buffer.
 struct DevBuf {
@@ -116,6 +144,7 @@ struct tgohip_ctx {
   std::vector<hipEvent_t> prof_ev;
   double prof_attn_ms = 0, prof_attn_bytes = 0;
   int64_t prof_attn_launches = 0;
+  void* scratch = nullptr;  // this device's address of the static split-K workspace
 };
 
 namespace {
@@ -463,9 +492,12 @@ tgohip_ctx* tgohip_open(int device) {
                              prop.gcnArchName);
     return nullptr;
   }
+  void* scr = nullptr;
+  if (scratch_setup(device, &scr)) return nullptr;
   auto* c = new tgohip_ctx();
   c->device = device;
   c->ncu = prop.multiProcessorCount;
+  c->scratch = scr;
   if (hipStreamCreate(&c->own_stream) != hipSuccess ||
       hipEventCreateWithFlags(&c->staged, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&c->ev0, hipEventDisableSystemFence) != hipSuccess ||
@@ -1115,6 +1147,26 @@ int tgohip_linear(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, 
   if (rc) return rc;
   return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
                       (float*)c->gemm_ws.p, c->gemm_ws.bytes, c->ncu, c->stream);
+}
+
+// tgohip_linear without allocating: the split-K partials go to the static
+// `scratch` array (kScratchBytes, this device's copy) instead of the
+// context's workspace. Same kernels, same splits, so the same result.
+int tgohip_linear_noalloc(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, void* y,
+                          int y_dtype) {
+  PackedWeight* w = handle_of(c, handle);
+  if (!w) return TGOHIP_EINVAL;
+  if (M < 0) return fail(TGOHIP_EINVAL, "linear_noalloc: M is " + std::to_string(M));
+  const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
+  if (ws > kScratchBytes)
+    return fail(TGOHIP_EINVAL, "linear_noalloc: M = " + std::to_string(M) + " over [" +
+                                   std::to_string(w->K) + "," + std::to_string(w->N) +
+                                   "] needs " + std::to_string(ws) + " bytes of split-K partials "
+                                   "and the static workspace holds " +
+                                   std::to_string(kScratchBytes) + "; use tgohip_linear");
+  if (!c->scratch) return fail(TGOHIP_ESTATE, "linear_noalloc: no workspace address for this device");
+  return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
+                      (float*)c->scratch, kScratchBytes, c->ncu, c->stream);
 }
 
 int tgohip_dequant(tgohip_ctx* c, int handle, float* y) {
