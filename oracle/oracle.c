@@ -22,8 +22,12 @@
  *   orc_quantize_int4_tgo parity unpinned at the bit level (accel
  *                         quant.Int4Quantize is absent). Format: 8 codes per u32,
  *                         element i of a word in bits 4i..4i+3, f16 scale and f16
- *                         integer zero per 128 flattened elements. Pinned only by
- *                         tgo's bound (tolerance.go:151-175) and round trips.
+ *                         integer zero per 128 flattened elements. Pinned by what
+ *                         the reference states of it: the step is the group's
+ *                         range over fifteen (tolerance.go:150-160; the tests
+ *                         check scale, zero and every code per group, and that
+ *                         range/16 is told apart), tgo's error bound
+ *                         (tolerance.go:151-175) and round trips.
  *   orc_dequant_int4_sym  the BASELINE pack (symmetric, group 32 along K), defined
  *                         by this build; pinned by closed form on tiny inputs.
  *   orc_*_f64             pinned: known answers of the internal/oracle test files.

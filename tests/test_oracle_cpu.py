@@ -301,6 +301,54 @@ def test_int4_tgo_layout_and_bound():
         assert abs(got[col] - exact[col]) <= bound + 1e-12
 
 
+def test_int4_tgo_quantizer_follows_the_range_over_fifteen_rule():
+    """What the mathematics fixes about the int4 triple (tolerance.go:150-160: "a group's
+    range over fifteen"): per group of 128 flattened elements the stored scale is
+    f16((max - min) / 15) (so a step of range/16 fails), the zero is round(-min / s)
+    clamped to [0, 15], and each code is round(x / s + z) clamped to [0, 15], so every
+    element not at a clamp reconstructs within half a step. Ties round to even (this
+    build's rule; accel's quantizer is absent and its bit layout parity unpinned)."""
+    rng = np.random.default_rng(9)
+    n = 128 * 24 + 40  # a ragged last group
+    w = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    w[128:256] += 0.04   # all-positive-ish group: the zero clamps low
+    w[256:384] = 0.125   # a flat group
+    c = np.empty((n + 7) // 8, np.uint32)
+    s = np.empty((n + 127) // 128, np.uint16)
+    z = np.empty_like(s)
+    L.orc_quantize_int4_tgo(P(w), n, P(c), P(s), P(z))
+    q = ((c[:, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).ravel()[:n]
+    for g in range(len(s)):
+        blk = w[g * 128:(g + 1) * 128]
+        mn, mx = np.float32(blk.min()), np.float32(blk.max())
+        step = np.float32((mx - mn) / np.float32(15))
+        want_s = oracle.f16_bits(np.float32(step if step > 0 else 1.0))
+        assert s[g] == want_s, g
+        assert s[g] != oracle.f16_bits(np.float32((mx - mn) / np.float32(16))) or step == 0
+        sv = float(np.float16(s.view(np.float16)[g]))
+        zv = float(np.float16(z.view(np.float16)[g]))
+        assert zv == min(15.0, max(0.0, float(np.round(-float(mn) / sv))))
+        want_q = np.clip(np.round(blk.astype(np.float64) / sv + zv), 0, 15)
+        assert np.array_equal(q[g * 128:(g + 1) * 128], want_q.astype(np.uint32)), g
+        back = (want_q - zv) * sv
+        inside = (want_q > 0) & (want_q < 15)
+        assert np.all(np.abs(back - blk)[inside] <= sv / 2 * (1 + 1e-6)), g
+    assert float(np.float16(s.view(np.float16)[2])) == 1.0  # flat group: step 1
+
+
+def test_int8_rounds_half_steps_to_even():
+    """The int8 rule on a constructed block: peak 127 gives the exact scale 1.0, so x/s
+    lands on half steps exactly; ties go to even (this build's rule, accel's being
+    invisible), and the codes saturate at +-127."""
+    w = np.zeros(32, np.float32)
+    w[:8] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 126.5]
+    q = np.empty(32, np.int8)
+    s = np.empty(1, np.uint16)
+    L.orc_quantize_int8(P(w), 32, P(q), P(s))
+    assert float(s.view(np.float16)[0]) == 1.0
+    assert q[:8].tolist() == [127, 2, 4, -2, -4, 0, 0, 126]
+
+
 def test_int4_sym_closed_form():
     """The BASELINE pack on a tiny hand-built plane: w[k][n] = (nibble - 8) * s[k/32][n]."""
     K, N = 64, 2
