@@ -60,6 +60,7 @@ C5_CHUNK = 1024
 C5_POOL = 330_000       # positions (86 GB of f16 K+V at 64 layers)
 HBM_PEAK = 8000.0       # GB/s, MI355X published
 PROFILE_STRIDE = 4      # attention launches timed: those of every 4th layer
+PROFILE_STEPS = 3       # steps with every kernel kind timed, after each timed phase
 MFMA_F16_PEAK = 2500.0  # TFLOP/s dense f16, MI355X published
 
 
@@ -87,6 +88,12 @@ def parse():
     p.add_argument("--cascade", type=int, default=2,
                    help="config 5: group decode rows whose page tables share a prefix when at "
                         "least this many do (0: off, every sequence reads its own prefix)")
+    p.add_argument("--phase", default="both", choices=["both", "mixed", "decode"],
+                   help="profiling runs: mixed steps only, or straight to the decode-only steps "
+                        "(the default line runs both)")
+    p.add_argument("--decode-steps", type=int, default=100,
+                   help="after the headline steps, this many decode-only steps (the 128 decoders "
+                        "with no prefill chunk) for the decode-dominated figures (0: skip)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="before the workload, run one plain f32 copy kernel (torch.neg) over this "
                         "many MiB: the known-size dispatch that scales the HBM byte counters")
@@ -157,6 +164,13 @@ class Workload:
         of synchronous mode."""
         out = 0
         started = 0
+        if getattr(self, "frozen", False):
+            for slot, done in produced:
+                if done:
+                    out += 1
+                    if tokens is not None:
+                        self.sched.feed(slot, tokens[slot])
+            return out
         for slot, done in produced:
             if not done:
                 continue
@@ -174,6 +188,14 @@ class Workload:
         self.admit_arrivals()
         return out
 
+    def decode_only(self):
+        """From here on every step is the decoders alone: the requests mid-prefill are
+        finished and nothing arrives or retires (each decoder's lease grows as it goes)."""
+        self.frozen = True
+        for slot in [s for s in self.target if s not in self.decoding]:
+            self.sched.finish(slot)
+            del self.target[slot]
+
     def step(self):
         """One synchronous step: (output tokens, prefill tokens, decodes, timings)."""
         produced, prefill, decodes, tm = self.sched.step()
@@ -187,7 +209,7 @@ class Workload:
         return out, prefill, decodes
 
 
-def run_steps(wl, ctx, steps, warmup, sync):
+def run_steps(wl, ctx, steps, warmup, sync, profile=True):
     """Warm-up steps, then exactly `steps` timed steps. Overlap mode keeps one step
     in flight while the host schedules the next; the pipeline starts empty and is
     drained inside the timed region, so the wall time covers exactly the timed
@@ -225,7 +247,8 @@ def run_steps(wl, ctx, steps, warmup, sync):
     ctx.sync()
     # HIP events around the attention launch of every 4th layer (each layer's
     # attention does the same work; each record leaves the device idle ~4 us)
-    ctx.set_profile(True, PROFILE_STRIDE)
+    if profile:
+        ctx.set_profile(True, PROFILE_STRIDE)
     t0 = time.perf_counter()
     out, pf, dc, dev_ms = run(steps, True)
     ctx.sync()
@@ -341,6 +364,71 @@ def run_c5(args, tgo_amd):
     }
 
 
+def kernel_table(ctx, tgo, kinds):
+    """Per-launch means of the profiled kernel kinds: duration, algorithmic bytes and flops,
+    and the fractions of the HBM and dense f16 MFMA peaks they reach."""
+    out = {}
+    for k in kinds:
+        ms, by, fl, n = ctx.profile_read_kernel(k)
+        if not n:
+            continue
+        avg = ms / n
+        gbs = by / n / (avg * 1e-3) / 1e9
+        tfs = fl / n / (avg * 1e-3) / 1e12
+        out[tgo.PROF_NAMES[k]] = dict(avg_ms=round(avg, 4), launches=n,
+                                      bytes=round(by / n), flops=round(fl / n),
+                                      gbps=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK, 4),
+                                      tflops=round(tfs, 1), mfma_frac=round(tfs / MFMA_F16_PEAK, 4))
+    return out
+
+
+def profile_kernels(wl, ctx, tgo, steps, sync):
+    """`steps` more steps with every kernel kind of every 4th layer bracketed by events
+    (not part of any timed figure)."""
+    kinds = (tgo.PROF_ATTN, tgo.PROF_QKV, tgo.PROF_O, tgo.PROF_GATEUP, tgo.PROF_DOWN,
+             tgo.PROF_LMHEAD)
+    ctx.set_profile_kernels(PROFILE_STRIDE, kinds)
+    run_steps(wl, ctx, steps, 0, sync, profile=False)
+    table = kernel_table(ctx, tgo, kinds)
+    ctx.set_profile(False)
+    return table
+
+
+def step_bytes(c, form, rows, members, attn_bytes_per_launch, precision):
+    """Algorithmic HBM bytes of one step: every weight once (the layers' projections, the
+    LM head, the embedding rows gathered), the KV the attention reads (from the profiled
+    launches, less their q in / out) and writes, and the logits written."""
+    d, f, V, L = c["hidden"], c["ffn"], c["vocab"], c["layers"]
+    qw, kw = c["heads"] * 128, c["kv_heads"] * 128
+    per_weight = {3: 0.5 + 2 / 32, 2: 0.5 + 4 / 128, 1: 1 + 2 / 32, 0: 2.0}[form]
+    layer_w = (d * (qw + 2 * kw) + qw * d + 2 * d * f + f * d) * per_weight
+    weights = L * layer_w + d * V * per_weight + rows * d * (1 + 2 / 32)
+    q_io = rows * c["heads"] * 128 * (4 if precision == 0 else 8)  # q in, out
+    kv_read = L * (attn_bytes_per_launch - q_io)
+    kv_write = L * rows * kw * 2 * 2
+    logits = members * V * 4
+    total = weights + kv_read + kv_write + logits
+    return total, dict(weights=round(weights), kv_read=round(kv_read), kv_write=round(kv_write),
+                       logits=round(logits))
+
+
+def recorded_mfma():
+    """MFMA counters per projection kernel on this workload (rocprofv3 --pmc), as profiles/
+    records them: dense f16 MFMA flops executed per dispatch (SQ_INSTS_VALU_MFMA_MOPS_F16 x
+    512) over the dispatch's duration, and the MFMA busy fraction
+    (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs))."""
+    path = os.path.join(ROOT, "profiles", "gemm_mfma_c4_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    out = {}
+    for line in open(path):
+        if line.startswith("mfma "):
+            _, step, name, tflops, frac, busy = line.split()
+            out.setdefault(step, {})[name] = dict(tflops=float(tflops), mfma_frac=float(frac),
+                                                  mfma_busy=float(busy))
+    return out or None
+
+
 def recorded_traffic():
     """HBM bytes per attention launch measured with rocprofv3 --pmc on this workload
     (FETCH_SIZE + WRITE_SIZE, each scaled by a copy probe), as profiles/ records it."""
@@ -381,6 +469,38 @@ def cpu_baseline(st, pages, max_pages, out_tokens, form):
                 seconds=t1 + t2)
 
 
+def run_decode_phase(wl, ctx, tgo, args):
+    """The decode-dominated step the north-star target is judged on: the same 128
+    decoders (their contexts grown by the timed steps) with no prefill chunk, 128 rows per
+    step. Timed like the headline (warm-up, then exactly decode_steps steps, attention
+    launches of every 4th layer bracketed by events); then a few steps with every kernel
+    timed. Whole-step HBM fraction = algorithmic bytes of a step (weights once, KV read and
+    written, logits) / the step's wall time / 8 TB/s."""
+    wl.decode_only()
+    el, out, pf, dc, dev_ms = run_steps(wl, ctx, args.decode_steps, 5, args.sync)
+    assert pf == 0 and dc == DECODERS * args.decode_steps, (pf, dc)
+    attn_ms, attn_bytes, launches = ctx.profile_read()
+    ctx.set_profile(False)
+    kernels = profile_kernels(wl, ctx, tgo, PROFILE_STEPS, args.sync)
+    ms = 1e3 * el / args.decode_steps
+    rows = DECODERS
+    total, parts = step_bytes(C4, args.form, rows, SLOTS, attn_bytes / max(launches, 1),
+                              args.precision)
+    gbs = total / (ms * 1e-3) / 1e9
+    avg_attn = attn_ms / max(launches, 1)
+    attn_gbs = attn_bytes / max(launches, 1) / (avg_attn * 1e-3) / 1e9
+    return dict(
+        workload="the 128 decoders of the headline run continuing alone (no prefill chunk): "
+                 "128 rows per step, contexts lognormal median 1024 grown by the steps before",
+        steps=args.decode_steps, ms_per_step=round(ms, 3), tok_per_s=round(out / el, 1),
+        device_ms_per_step=round(dev_ms / args.decode_steps, 3),
+        hbm_bytes_per_step=round(total), bytes=parts, hbm_gbps=round(gbs, 1),
+        hbm_frac=round(gbs / HBM_PEAK, 4),
+        attention=dict(avg_launch_ms=round(avg_attn, 4), gbps=round(attn_gbs, 1),
+                       frac=round(attn_gbs / HBM_PEAK, 4), launches=launches),
+        kernels=kernels)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -411,6 +531,11 @@ def main():
           (setup_s, DECODERS, np.mean([x for x in wl.contexts if x > 0])), file=sys.stderr,
           flush=True)
 
+    if args.phase == "decode":
+        decode = run_decode_phase(wl, ctx, tgo_amd, args)
+        ctx.close()
+        print(json.dumps(dict(phase="decode", decode_step=decode)), flush=True)
+        return
     elapsed, total_out, total_pf, total_dc, dev_ms = run_steps(wl, ctx, args.steps, args.warmup,
                                                                args.sync)
     attn_ms, attn_bytes, launches = ctx.profile_read()
@@ -418,6 +543,10 @@ def main():
     last_st, last_pages, maxp = wl.sched.last_step()
     # the CPU leg is charged the mean output tokens of a timed step
     last_out = total_out / args.steps
+    mixed_kernels = profile_kernels(wl, ctx, tgo_amd, PROFILE_STEPS, args.sync)
+    decode = None
+    if args.decode_steps and args.phase == "both":
+        decode = run_decode_phase(wl, ctx, tgo_amd, args)
 
     avg_attn_ms = attn_ms / max(launches, 1)
     achieved = (attn_bytes / max(launches, 1)) / (avg_attn_ms * 1e-3) / 1e9
@@ -465,6 +594,9 @@ def main():
             "launches": launches,
         },
         "cpu_baseline": None,
+        "kernels": mixed_kernels,
+        "decode_step": decode,
+        "mfma_counters": recorded_mfma(),
     }
     ctx.close()
     if not args.no_cpu:

@@ -361,6 +361,25 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
 int tgohip_set_profile(tgohip_ctx* ctx, int on);
 int tgohip_profile_read(tgohip_ctx* ctx, double* attn_ms, double* attn_bytes,
                         int64_t* launches);
+
+/* The same for any of the step's kernels (measurement helper, no counterpart in
+ * the reference; bench/bench.go:60-74 times whole steps only): mask has bit
+ * TGOHIP_PROF_<kind> set for each kind timed, in every stride-th layer (the LM
+ * head once per step). Reading a kind gives its summed duration, algorithmic
+ * bytes (weights once, activations in and out; attention as above) and flops
+ * (2*M*K*N; attention 4*d_h*H per visible query-key pair) over its launches. */
+enum {
+  TGOHIP_PROF_ATTN = 0,
+  TGOHIP_PROF_QKV = 1,
+  TGOHIP_PROF_O = 2,
+  TGOHIP_PROF_GATEUP = 3,
+  TGOHIP_PROF_DOWN = 4,
+  TGOHIP_PROF_LMHEAD = 5,
+  TGOHIP_PROF_KINDS = 6
+};
+int tgohip_set_profile_kernels(tgohip_ctx* ctx, int stride, int mask);
+int tgohip_profile_read_kernel(tgohip_ctx* ctx, int kind, double* ms, double* bytes,
+                               double* flops, int64_t* launches);
 /* Fills positions [0, positions) of every layer's K and V with seeded f16
  * N(0,1)*sigma: the context of sequences admitted already prefilled. */
 int tgohip_kv_synth(tgohip_ctx* ctx, uint64_t seed, double sigma, int positions);

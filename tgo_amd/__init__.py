@@ -16,6 +16,8 @@ LIB_PATH = os.path.join(HERE, "libtgohip.so")
 
 FORM_F16, FORM_I8, FORM_I4_TGO, FORM_I4_SYM = 0, 1, 2, 3
 F32, F16 = 0, 1
+PROF_ATTN, PROF_QKV, PROF_O, PROF_GATEUP, PROF_DOWN, PROF_LMHEAD = range(6)
+PROF_NAMES = ("attention", "qkv", "o", "gateup", "down", "lm_head")
 
 EINVAL, ENOMEM, EDEVICE, ESTATE, EEXHAUSTED, ENOSLOT = -1, -2, -3, -4, -5, -6
 
@@ -120,6 +122,8 @@ def lib():
         "tgohip_sched_collect": (I, [P, P, P, P, ctypes.POINTER(Timings)]),
         "tgohip_set_profile": (I, [P, I]),
         "tgohip_profile_read": (I, [P, P, P, P]),
+        "tgohip_set_profile_kernels": (I, [P, I, I]),
+        "tgohip_profile_read_kernel": (I, [P, I, P, P, P, P]),
         "tgohip_kv_synth": (I, [P, U64, D, I]),
         "tgohip_to_f16": (ctypes.c_size_t, [P, P, ctypes.c_size_t]),
         "tgohip_quantize_int8": (None, [P, ctypes.c_size_t, P, P]),
@@ -486,6 +490,20 @@ class Context:
     def set_profile(self, on, stride=1):
         """Time the attention launch of every `stride`-th layer (HIP events)."""
         check(lib().tgohip_set_profile(self.h, stride if on else 0))
+
+    def set_profile_kernels(self, stride, kinds):
+        """Time the launches of the kernel kinds named (PROF_*) in every stride-th layer."""
+        mask = 0
+        for k in kinds:
+            mask |= 1 << k
+        check(lib().tgohip_set_profile_kernels(self.h, stride, mask))
+
+    def profile_read_kernel(self, kind):
+        """-> (ms, algorithmic bytes, flops, launches) summed over the timed launches."""
+        ms, by, fl, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        check(lib().tgohip_profile_read_kernel(self.h, kind, ctypes.byref(ms), ctypes.byref(by),
+                                               ctypes.byref(fl), ctypes.byref(n)))
+        return ms.value, by.value, fl.value, n.value
 
     def profile_read(self):
         ms, by, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()

@@ -12,21 +12,14 @@
 //                       restatement's generator
 #include "../common.h"
 
+#include <algorithm>
+
 namespace tgohip {
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
-}
-
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
 }
 
 // h[t, :] = table[ids[t], :] (f16) or q * scale (int8, one scale per 32
@@ -51,19 +44,32 @@ __global__ void embed_kernel(const uint32_t* ids, const void* table, const uint1
 }
 
 // out[r, :] = x[src(r), :] * rsqrt(mean(x^2) + eps) * g, stored f16 or f32.
-// src(r) = rows ? rows[r] : r. One 256-thread block per row.
+// src(r) = rows ? rows[r] : r. One block per row, a float4 per thread (up to
+// 1024 threads; wider rows loop): every load of a row is in flight at once.
 // With nsplit > 0 the residual add of a split-K projection is still pending:
 // x[src, :] += sum_s part[s][src, :] (summed in split order, as
 // gemm_reduce_kernel would) is done here first and written back to x.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(float* x, const uint32_t* rows,
-                                                      const float* g, int w, float eps,
-                                                      void* out, int out_f16, const float* part,
-                                                      int nsplit, size_t plane) {
-  __shared__ float red[4];
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; i++) t += red[i];
+  return t;
+}
+
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t* rows,
+                                                       const float* g, int w, float eps,
+                                                       void* out, int out_f16, const float* part,
+                                                       int nsplit, size_t plane) {
+  __shared__ float red[16];
   const int r = blockIdx.x;
+  const int step = blockDim.x * 4;
   const size_t src = (size_t)(rows ? rows[r] : (uint32_t)r) * w;
   float ss = 0.f;
-  for (int i = threadIdx.x * 4; i < w; i += 1024) {
+  for (int i = threadIdx.x * 4; i < w; i += step) {
     float4_t v = *(const float4_t*)(x + src + i);
     if (nsplit > 0) {
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -73,9 +79,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float* x, const uint32_t* 
     }
     ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
   }
-  ss = block_sum256(ss, red);
+  ss = block_sum(ss, red);
   const float sc = 1.0f / sqrtf(ss / (float)w + eps);
-  for (int i = threadIdx.x * 4; i < w; i += 1024) {
+  for (int i = threadIdx.x * 4; i < w; i += step) {
     const float4_t v = *(const float4_t*)(x + src + i);
     const float4_t gg = *(const float4_t*)(g + i);
     float4_t o;
@@ -129,7 +135,7 @@ __device__ __forceinline__ float half_wave_sum(float v) {
 // with 16-byte loads. (Loading a batch of a wave's rows before working on any
 // measured 65% slower.)
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
-  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6 | blockIdx.y << 2;
   const int half = lane >> 5, l32 = lane & 31;
   const int NH = a.H + 2 * a.Hkv;
   const int W = NH * kHeadDim;
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   int cpos = -1;
   float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
   const double inv0 = a.inv_freq[2 * l32], inv1 = a.inv_freq[2 * l32 + 1];
-  for (int k = wave; 2 * k < NH; k += 4) {
+  for (int k = wave; 2 * k < NH; k += 4 * gridDim.y) {
     const int hh = 2 * k + half;
     if (hh >= NH) continue;  // an odd head count leaves the last half wave idle
     // split-K projection: the row is the sum of the partial planes, in split order
@@ -403,14 +409,19 @@ void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t*
 void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
                     float eps, void* out, int out_f16, hipStream_t st, const float* part,
                     int nsplit, size_t plane) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, st, x, rows, g, w, eps, out, out_f16,
-                     part, nsplit, plane);
+  const int threads = std::min(1024, std::max(64, (w / 4 + 63) / 64 * 64));
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(threads), 0, st, x, rows, g, w, eps, out,
+                     out_f16, part, nsplit, plane);
 }
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(derive_rows_kernel, dim3(a.B + 1), dim3(256), 0, st, a);
 }
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
-  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T), dim3(256), 0, st, a);
+  // A block's 4 waves take 8 heads; enough blocks per row to fill the chip
+  // when the rows are few (a decode step), one per row otherwise.
+  const int groups = (a.H + 2 * a.Hkv + 7) / 8;
+  const int gy = T >= 512 ? 1 : groups;
+  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T, gy), dim3(256), 0, st, a);
 }
 void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
                    hipStream_t st, int keep_idle, double* margin) {

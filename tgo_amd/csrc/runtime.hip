@@ -138,12 +138,15 @@ struct tgohip_ctx {
   std::vector<void*> allocs;  // weight and gain allocations owned by the context
   std::map<int, PackedWeight> handles;
   int next_handle = 1;
-  // profiling: HIP events around every attention launch of a step
+  // profiling: HIP events around the launches of the kernels in prof_mask
+  // (TGOHIP_PROF_* bits) in every prof_stride-th layer of a step
   bool profile = false;
-  int prof_stride = 1;  // time the attention launch of every prof_stride-th layer
-  std::vector<hipEvent_t> prof_ev;
-  double prof_attn_ms = 0, prof_attn_bytes = 0;
-  int64_t prof_attn_launches = 0;
+  int prof_stride = 1;
+  int prof_mask = 1 << TGOHIP_PROF_ATTN;
+  std::vector<hipEvent_t> prof_ev;  // [2 sets][layers][kinds][begin, end]
+  double prof_ms[TGOHIP_PROF_KINDS] = {}, prof_bytes[TGOHIP_PROF_KINDS] = {},
+         prof_flops[TGOHIP_PROF_KINDS] = {};
+  int64_t prof_launches[TGOHIP_PROF_KINDS] = {};
   void* scratch = nullptr;  // this device's address of the static split-K workspace
 };
 
@@ -784,13 +787,35 @@ namespace {
 // One step's device work, enqueued on c->stream without waiting: the ports
 // staged and uploaded, every kernel launched, ev_begin / ev_end recorded
 // around them. The argmax of every member is left in c->argmax.
+// Algorithmic bytes and flops of one launch of each profiled kernel kind.
+struct ProfStep {
+  double bytes[TGOHIP_PROF_KINDS] = {};
+  double flops[TGOHIP_PROF_KINDS] = {};
+};
+
 struct StepLaunch {
   const int32_t* feed = nullptr;  // ids with bit 31 set take feed[member] (device)
   int keep_idle = 0;              // argmax leaves the entries of idle members as they are
   hipEvent_t ev_begin = nullptr, ev_end = nullptr;
-  int prof_set = 0;               // which set of attention profile events
-  double attn_bytes = 0;          // out: algorithmic bytes of one attention launch
+  int prof_set = 0;               // which set of profile events
+  ProfStep prof;                  // out: per-launch algorithmic bytes and flops
 };
+
+// A projection's algorithmic bytes (weights once, activations in, output out;
+// a residual add reads and writes h) and flops, 2*M*K*N.
+void gemm_algorithmic(const PackedWeight& w, int M, bool x_f32, int epi, double& bytes, double& flops) {
+  const double halves = (double)packed_scale_halves(w.form, w.K, w.N);
+  bytes = (double)packed_payload_bytes(w.form, w.K, w.N) +
+          halves * 2 * (w.form == TGOHIP_FORM_I4_TGO ? 2 : 1) + (double)M * w.K * (x_f32 ? 4 : 2);
+  switch (epi) {
+    case EPI_RESID: bytes += (double)M * w.N * 8; break;
+    case EPI_SWIGLU_F16: bytes += (double)M * w.N / 2 * 2; break;
+    case EPI_SWIGLU_F32: bytes += (double)M * w.N / 2 * 4; break;
+    case EPI_F16: bytes += (double)M * w.N * 2; break;
+    default: bytes += (double)M * w.N * 4; break;
+  }
+  flops = 2.0 * M * w.K * w.N;
+}
 
 int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   if (!c->configured) return fail(TGOHIP_ESTATE, "step: configure the context first");
@@ -878,23 +903,45 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   const size_t wsb = c->gemm_ws.bytes;
 
   // Algorithmic bytes of one attention launch: every cached position a
-  // claimed row reads, once (K and V, all kv heads), plus q read and out written.
-  o.attn_bytes = 0;
+  // claimed row reads, once (K and V, all kv heads), plus q read and out written;
+  // flops 4 * d_h * H per visible (query, key) pair.
+  o.prof = ProfStep();
   hipEvent_t* pev = nullptr;
+  constexpr int NK = TGOHIP_PROF_KINDS;
   if (c->profile) {
-    for (int b = 0; b < B; b++)
-      if (s->extents[b] > 0) o.attn_bytes += (double)s->lengths[b] * m.kv_heads * kHeadDim * 2 * 2;
-    o.attn_bytes += (double)plan.claimed * m.heads * kHeadDim * (f32act ? 4 + 4 : 2 + 2);  // q in, out
-    o.attn_bytes -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
-    while ((int)c->prof_ev.size() < 4 * m.layers) {
+    double& ab = o.prof.bytes[TGOHIP_PROF_ATTN];
+    double pairs = 0;
+    for (int b = 0; b < B; b++) {
+      const double L = s->lengths[b], n = s->extents[b];
+      if (n > 0) ab += L * m.kv_heads * kHeadDim * 2 * 2;
+      pairs += n * (L - n) + n * (n + 1) / 2;
+    }
+    ab += (double)plan.claimed * m.heads * kHeadDim * (f32act ? 4 + 4 : 2 + 2);  // q in, out
+    ab -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
+    o.prof.flops[TGOHIP_PROF_ATTN] = 4.0 * kHeadDim * m.heads * pairs;
+    const Layer& L0 = c->layers[0];
+    gemm_algorithmic(L0.qkv, T, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_QKV], o.prof.flops[TGOHIP_PROF_QKV]);
+    gemm_algorithmic(L0.wo, T, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_O], o.prof.flops[TGOHIP_PROF_O]);
+    gemm_algorithmic(L0.gateup, T, f32act, f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16,
+                     o.prof.bytes[TGOHIP_PROF_GATEUP], o.prof.flops[TGOHIP_PROF_GATEUP]);
+    gemm_algorithmic(L0.down, T, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
+    gemm_algorithmic(c->lm_head, B, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
+                     o.prof.flops[TGOHIP_PROF_LMHEAD]);
+    while (c->prof_ev.size() < (size_t)2 * m.layers * NK * 2) {
       // timing only: no system-scope fence (an L2 write-back each, which
       // left a ~6 us gap on both sides of every attention launch)
       hipEvent_t e;
       TGOHIP_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
       c->prof_ev.push_back(e);
     }
-    pev = c->prof_ev.data() + (size_t)o.prof_set * 2 * m.layers;
+    pev = c->prof_ev.data() + (size_t)o.prof_set * m.layers * NK * 2;
   }
+  // events around kernel `kind` of layer l, when profiled
+  auto mark = [&](int kind, int l, int end) -> int {
+    if (pev && (c->prof_mask >> kind & 1) && (kind == TGOHIP_PROF_LMHEAD || l % c->prof_stride == 0))
+      TGOHIP_HIP(hipEventRecord(pev[((size_t)l * NK + kind) * 2 + end], st));
+    return 0;
+  };
   launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
   uint32_t* d_rowpos = (uint32_t*)c->rows.p;
   uint32_t* d_rowslot = d_rowpos + T;
@@ -912,9 +959,11 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     const Layer& L = c->layers[l];
     launch_rmsnorm(h, nullptr, T, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
     int qkv_split = 0;
+    if ((rc = mark(TGOHIP_PROF_QKV, l, 0))) return rc;
     if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, T, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
                            &qkv_split)))
       return rc;
+    if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
     QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
                   split_plane_stride(T, (m.heads + 2 * m.kv_heads) * kHeadDim), L.g_q, L.g_k,
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
@@ -923,27 +972,34 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16};
     launch_qk_rope_kv(qa, T, st);
-    const bool timed = pev && l % c->prof_stride == 0;
-    if (timed) TGOHIP_HIP(hipEventRecord(pev[2 * l], st));
+    if ((rc = mark(TGOHIP_PROF_ATTN, l, 0))) return rc;
     if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
-    if (timed) TGOHIP_HIP(hipEventRecord(pev[2 * l + 1], st));
+    if ((rc = mark(TGOHIP_PROF_ATTN, l, 1))) return rc;
+    if ((rc = mark(TGOHIP_PROF_O, l, 0))) return rc;
     if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
+    if ((rc = mark(TGOHIP_PROF_O, l, 1))) return rc;
     launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    if ((rc = mark(TGOHIP_PROF_GATEUP, l, 0))) return rc;
     if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, T, c->act.p,
                            f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
       return rc;
+    if ((rc = mark(TGOHIP_PROF_GATEUP, l, 1))) return rc;
     // the last layer's residual add completes here (the head reads only Last rows)
+    if ((rc = mark(TGOHIP_PROF_DOWN, l, 0))) return rc;
     if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st,
                            l + 1 < m.layers ? &pend : nullptr)))
       return rc;
+    if ((rc = mark(TGOHIP_PROF_DOWN, l, 1))) return rc;
     if (l + 1 == m.layers) pend = 0;
   }
   launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p, actf16, st);
+  if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 0))) return rc;
   if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
+  if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 1))) return rc;
   launch_zero_idle((float*)c->logits.p, B, m.vocab, d_ext, st);
   launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st, o.keep_idle,
                 (double*)c->margin.p);
@@ -952,18 +1008,24 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   return 0;
 }
 
-// Adds one landed step's attention launches to the profile totals.
-int profile_collect(tgohip_ctx* c, int prof_set, double attn_bytes) {
-  if (!c->profile || c->prof_ev.size() < (size_t)4 * c->cfg.layers) return 0;
-  const hipEvent_t* pev = c->prof_ev.data() + (size_t)prof_set * 2 * c->cfg.layers;
-  int timed = 0;
-  for (int l = 0; l < c->cfg.layers; l += c->prof_stride, timed++) {
-    float ms = 0;
-    TGOHIP_HIP(hipEventElapsedTime(&ms, pev[2 * l], pev[2 * l + 1]));
-    c->prof_attn_ms += ms;
+// Adds one landed step's profiled launches to the totals.
+int profile_collect(tgohip_ctx* c, int prof_set, const ProfStep& ps) {
+  constexpr int NK = TGOHIP_PROF_KINDS;
+  const int L = c->cfg.layers;
+  if (!c->profile || c->prof_ev.size() < (size_t)2 * L * NK * 2) return 0;
+  const hipEvent_t* pev = c->prof_ev.data() + (size_t)prof_set * L * NK * 2;
+  for (int k = 0; k < NK; k++) {
+    if (!(c->prof_mask >> k & 1)) continue;
+    const int stride = k == TGOHIP_PROF_LMHEAD ? L : c->prof_stride;
+    for (int l = 0; l < L; l += stride) {
+      float ms = 0;
+      TGOHIP_HIP(hipEventElapsedTime(&ms, pev[((size_t)l * NK + k) * 2], pev[((size_t)l * NK + k) * 2 + 1]));
+      c->prof_ms[k] += ms;
+      c->prof_launches[k]++;
+      c->prof_bytes[k] += ps.bytes[k];
+      c->prof_flops[k] += ps.flops[k];
+    }
   }
-  c->prof_attn_launches += timed;
-  c->prof_attn_bytes += attn_bytes * timed;
   return 0;
 }
 
@@ -988,7 +1050,7 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
     TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)s->batch * m.vocab * 4, hipMemcpyDeviceToHost));
   if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)s->batch * 4, hipMemcpyDeviceToHost));
   const auto t_end = clk::now();
-  if ((rc = profile_collect(c, 0, o.attn_bytes))) return rc;
+  if ((rc = profile_collect(c, 0, o.prof))) return rc;
   if (tm) {
     float dev_ms = 0;
     (void)hipEventElapsedTime(&dev_ms, c->ev0, c->ev1);
@@ -1211,7 +1273,8 @@ struct InflightStep {
   std::vector<char> done;        // the slot's prompt is scored once the step lands
   int parity = 0;
   int32_t prefill = 0, decodes = 0;
-  double submit_ms = 0, attn_bytes = 0;
+  double submit_ms = 0;
+  ProfStep prof;
 };
 
 static void sync_proj(SchedSlot& s) {
@@ -1607,7 +1670,7 @@ int tgohip_sched_submit(tgohip_sched* s, int32_t* out_slot, int32_t* out_done,
   TGOHIP_HIP(hipMemcpyAsync(s->amax_host[f.parity], c->argmax.p, (size_t)n * 4,
                             hipMemcpyDeviceToHost, c->stream));
   TGOHIP_HIP(hipEventRecord(s->ev[f.parity][2], c->stream));
-  f.attn_bytes = o.attn_bytes;
+  f.prof = o.prof;
   // the books as they will stand once this step lands
   int produced = 0;
   for (int i = 0; i < nw; i++) {
@@ -1684,7 +1747,7 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
       st = SchedSlot();
     }
   }
-  if ((rc = profile_collect(s->ctx, f.parity, f.attn_bytes))) return rc;
+  if ((rc = profile_collect(s->ctx, f.parity, f.prof))) return rc;
   if (tm) {
     float dev_ms = 0;
     (void)hipEventElapsedTime(&dev_ms, s->ev[f.parity][0], s->ev[f.parity][1]);
@@ -1703,21 +1766,38 @@ int tgohip_sched_collect(tgohip_sched* s, int32_t* out_slot, int32_t* out_token,
 // ===========================================================================
 extern "C" {
 
+int tgohip_set_profile_kernels(tgohip_ctx* c, int stride, int mask) {
+  if (stride < 0) return fail(TGOHIP_EINVAL, "profile: " + std::to_string(stride) + " is not a layer stride");
+  if (mask < 0 || mask >= (1 << TGOHIP_PROF_KINDS))
+    return fail(TGOHIP_EINVAL, "profile: kernel mask " + std::to_string(mask) + " names no kernel kinds");
+  c->profile = stride != 0 && mask != 0;
+  c->prof_stride = stride > 0 ? stride : 1;
+  c->prof_mask = mask;
+  for (int k = 0; k < TGOHIP_PROF_KINDS; k++) {
+    c->prof_ms[k] = c->prof_bytes[k] = c->prof_flops[k] = 0;
+    c->prof_launches[k] = 0;
+  }
+  return 0;
+}
+
 int tgohip_set_profile(tgohip_ctx* c, int on) {
-  if (on < 0) return fail(TGOHIP_EINVAL, "profile: " + std::to_string(on) + " is not a layer stride");
-  c->profile = on != 0;
-  c->prof_stride = on > 0 ? on : 1;
-  c->prof_attn_ms = 0;
-  c->prof_attn_bytes = 0;
-  c->prof_attn_launches = 0;
+  return tgohip_set_profile_kernels(c, on, 1 << TGOHIP_PROF_ATTN);
+}
+
+int tgohip_profile_read_kernel(tgohip_ctx* c, int kind, double* ms, double* bytes, double* flops,
+                               int64_t* launches) {
+  if (kind < 0 || kind >= TGOHIP_PROF_KINDS)
+    return fail(TGOHIP_EINVAL, "profile: no kernel kind " + std::to_string(kind));
+  *ms = c->prof_ms[kind];
+  *bytes = c->prof_bytes[kind];
+  *flops = c->prof_flops[kind];
+  *launches = c->prof_launches[kind];
   return 0;
 }
 
 int tgohip_profile_read(tgohip_ctx* c, double* attn_ms, double* attn_bytes, int64_t* launches) {
-  *attn_ms = c->prof_attn_ms;
-  *attn_bytes = c->prof_attn_bytes;
-  *launches = c->prof_attn_launches;
-  return 0;
+  double flops = 0;
+  return tgohip_profile_read_kernel(c, TGOHIP_PROF_ATTN, attn_ms, attn_bytes, &flops, launches);
 }
 
 // Fills positions [0, positions) of every layer of the K and V pools with

@@ -3,6 +3,15 @@
     python -m tgo_amd.prof stats <dir>/<name>_kernel_stats.csv
         per-kernel calls, total and average duration (from --kernel-trace --stats
         --output-format csv).
+    python -m tgo_amd.prof mfma <counter_collection.csv> <label>
+        per projection of the step (QKV, O, gate/up, down, LM head, told apart by their
+        place in the layer's launch sequence): dispatches, mean duration, the dense f16
+        MFMA flops executed (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512) per second and as a
+        fraction of 2.5 PFLOP/s, and the MFMA busy fraction
+        (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs): the CSV's
+        GRBM_GUI_ACTIVE is the sum over the 8 XCDs, each counting the dispatch's cycles,
+        which its ratio to the duration shows), from one rocprofv3 --pmc pass over those
+        three counters.
     python -m tgo_amd.prof pmc <fetch_counter_collection.csv> <write_counter_collection.csv>
         per-kernel mean FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by
         what the same counter reads for the copy-probe dispatch (torch.neg over a
@@ -60,9 +69,84 @@ def pmc(fetch_path, write_path, probe_mib):
     print("traffic_bytes_per_launch attn_kernel: %.0f" % attn)
 
 
+MFMA_PEAK_TFLOPS = 2500.0
+SIMDS = 1024  # 256 CUs x 4
+XCDS = 8      # GRBM_GUI_ACTIVE is reported summed over the XCDs
+
+
+def label_projections(names):
+    """The projection each GEMM dispatch computes, from the step's launch order: per layer
+    rmsnorm, QKV, qk_rope_kv, attention (+ combine), O, rmsnorm, gate/up, down; after the
+    last layer a gathered rmsnorm and the LM head, followed by zero_idle_rows_kernel."""
+    labels = [None] * len(names)
+    prev_gemm = None
+    for i, n in enumerate(names):
+        if "gemm_reduce" in n or "repack" in n or not ("gemm_" in n):
+            continue
+        before = next((names[j] for j in range(i - 1, -1, -1)
+                       if "gemm_reduce" not in names[j]), "")
+        after = names[i + 1] if i + 1 < len(names) else ""
+        if "zero_idle" in after:
+            lab = "lm_head"
+        elif "attn_" in before:
+            lab = "o"
+        elif "gemm_" in before:
+            lab = "down"
+        elif "rmsnorm" in before:
+            lab = "gateup" if prev_gemm == "o" else "qkv"
+        else:
+            lab = None
+        labels[i] = lab
+        prev_gemm = lab
+    return labels
+
+
+def mfma(path, label):
+    per = collections.defaultdict(dict)  # dispatch -> {counter: value, name, t}
+    for r in csv.DictReader(open(path)):
+        d = per[int(r["Dispatch_Id"])]
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        d["name"] = short(r["Kernel_Name"])
+        d["ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+    ids = sorted(per)
+    names = [per[i]["name"] for i in ids]
+    labels = label_projections(names)
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    for i, lab in zip(ids, labels):
+        if lab is None:
+            continue
+        d = per[i]
+        a = agg[lab]
+        a["n"] += 1
+        a["ns"] += d["ns"]
+        a["mops"] += d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0)
+        a["busy"] += d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        a["gui"] += d.get("GRBM_GUI_ACTIVE", 0.0)
+        a["kernel"] = d["name"]
+    print("%-8s %-44s %5s %10s %7s %12s %9s %9s" % ("proj", "kernel", "disp", "avg_us", "GHz",
+                                                    "mfma_TFLOP/s", "of_peak", "busy"))
+    for lab in ("qkv", "o", "gateup", "down", "lm_head"):
+        a = agg.get(lab)
+        if not a:
+            continue
+        tflops = a["mops"] * 512 / (a["ns"] * 1e-9) / 1e12
+        busy = a["busy"] / (a["gui"] / XCDS * SIMDS) if a["gui"] else 0.0
+        print("%-8s %-44s %5d %10.2f %7.3f %12.1f %9.4f %9.4f" % (
+            lab, a["kernel"][:44], a["n"], a["ns"] / a["n"] / 1e3, a["gui"] / XCDS / a["ns"],
+            tflops, tflops / MFMA_PEAK_TFLOPS, busy))
+    for lab in ("qkv", "o", "gateup", "down", "lm_head"):
+        a = agg.get(lab)
+        if a:
+            tflops = a["mops"] * 512 / (a["ns"] * 1e-9) / 1e12
+            busy = a["busy"] / (a["gui"] / XCDS * SIMDS) if a["gui"] else 0.0
+            print("mfma %s %s %.1f %.4f %.4f" % (label, lab, tflops, tflops / MFMA_PEAK_TFLOPS, busy))
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2])
+    elif sys.argv[1] == "mfma":
+        mfma(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
     else:
