@@ -82,6 +82,18 @@ struct DevBuf {
                                      hipGetErrorString(e));
     }
     bytes = n;
+    // TGOHIP_DEBUG_NAN_FILL=1: every activation and workspace buffer starts as
+    // all-ones bytes (NaN in f32 and f16), so a kernel that reads memory no
+    // earlier kernel wrote shows up as NaN logits or changed tokens.
+    static const bool nan_fill = [] {
+      const char* v = getenv("TGOHIP_DEBUG_NAN_FILL");
+      return v && atoi(v) != 0;
+    }();
+    if (nan_fill) {
+      e = hipMemset(p, 0xff, n);
+      if (e == hipSuccess) e = hipDeviceSynchronize();
+      if (e != hipSuccess) return fail(TGOHIP_EDEVICE, hip_message(e, "debug fill"));
+    }
     return 0;
   }
   void release() {
