@@ -63,7 +63,7 @@ struct AttnCombine {
 
 constexpr int kAttnTile = 64;     // positions staged in LDS per iteration
 constexpr int kAttnSplitDecode = 2560;   // positions per part of a split decode-style item
-constexpr int kAttnSplitPrefill = 3072;  // positions per part of a split prefill-style item
+constexpr int kAttnSplitPrefill = 2048;  // positions per part of a split prefill-style item
 constexpr int kAttnSplitShared = 512;    // positions per part of a shared-prefix item
 constexpr int kAttnRowsP = 128;   // rows per prefill-style item (4 waves x 32)
 constexpr int kHeadDim = 128;
