@@ -154,6 +154,44 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
         ctx.weight_free(h)
 
 
+@pytest.mark.parametrize("KN", [(4096, 6144), (12288, 4096), (4096, 24576), (4096, 151936)])
+def test_small_m_kernel_against_its_operands(ctx, torch_gpu, KN):
+    """The small-M kernels (at most 32 rows; 1-8 rows on the 16x16x32 pairing) at the
+    8B projection shapes, 16 waves per column block (QKV [4096, 6144], down [12288, 4096])
+    and 4 (gate/up [4096, 24576], LM head [4096, 151936]): f32 output on sampled columns
+    against the f64 product of the same operands; repeated calls bit-equal; the f16 output
+    is the f16 rounding of the same sums."""
+    torch = torch_gpu
+    import tgo_amd
+    K, N = KN
+    h = ctx.weight_synth(3, K, N, 11, 5, 0.02)
+    try:
+        cols = torch.arange(0, N, max(1, N // 96), device="cuda")
+        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        ctx.dequant_f16(h, wf)
+        wc = wf[:, cols].double()
+        del wf
+        for M in (1, 3, 8, 9, 32):
+            print("small-M linear [%d,%d] M=%d" % (K, N, M), flush=True)
+            x = torch.randn(M, K, device="cuda").half()
+            ys = []
+            for _ in range(3):
+                y = torch.full((M, N), float("nan"), device="cuda")
+                ctx.linear(h, x, M, y, x_dtype=tgo_amd.F16)
+                ys.append(y)
+            y16 = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+            ctx.linear(h, x, M, y16, x_dtype=tgo_amd.F16, y_dtype=tgo_amd.F16)
+            torch.cuda.synchronize()
+            assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2]), M
+            assert torch.equal(y16, ys[0].half()), M
+            ref = x.double() @ wc
+            mag = x.double().abs() @ wc.abs()
+            tol = 4 * (K ** 0.5) * 2.0 ** -24 * mag
+            assert bool(((ys[0][:, cols].double() - ref).abs() <= tol).all()), M
+    finally:
+        ctx.weight_free(h)
+
+
 @pytest.mark.parametrize("M", [33, 47, 96, 131, 300, 1000, 1152])
 @pytest.mark.parametrize("KN", [(2048, 416), (512, 4096), (512, 3712)])
 @pytest.mark.parametrize("form", [3, 2, 1])

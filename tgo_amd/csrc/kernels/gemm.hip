@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace tgohip {
 
@@ -832,31 +833,71 @@ int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t s
 }
 
 // ---- small M: the weight stream is the cost ---------------------------------
-// At most 32 rows. A workgroup owns CB 32-column blocks (two for the SwiGLU
-// epilogue, which pairs gate and up blocks; one otherwise, for more
-// workgroups) over the whole of K; its waves each stream an equal share of the
-// k-steps with gemv_depth<FORM>() k-steps of loads in flight, so no
-// split-K pass is needed. The activation rows are the MFMA A operand straight
-// from global memory (small and L2-resident; rows >= M are zero). The waves'
-// partial sums meet in LDS and are added in wave order, so the result is
-// deterministic.
+// At most 32 activation rows. A workgroup owns CB 32-column blocks (two for
+// the SwiGLU epilogue, which pairs gate and up blocks) over all of K; its W
+// waves each stream one contiguous share of the k-steps (K/64/W of them) as
+// a run of 1 KiB (int4) weight bursts with gemv_depth<FORM>() k-steps of
+// loads in flight, computing on the oldest while the rest arrive. The waves'
+// sums meet in LDS and are added in wave order, so the result is
+// deterministic and one launch does the whole product.
+//   Staged (1-8 rows, M*(K+8)*2 <= kGemvStageBytes): the activation rows are
+//     copied into LDS once per workgroup (after the first weight loads are
+//     issued; rows K + 8 halves apart, so the rows a read takes sit in
+//     different banks) and the MFMA A operand is read from there, so the weight stream
+//     is the only vector-memory traffic in the loop (measured at M = 1: LM
+//     head 88 -> 65 us, gate/up 17 -> 14 us against A loads from global
+//     memory). The product is v_mfma_f32_16x16x32_f16, half the matrix work
+//     per weight of 32x32x16: its hardware k slot (kq = lane/16, e) meets the
+//     weight lane whose fragment holds column n + 16 (kq % 2), k offset
+//     8 (kq / 2) + e of the substep, so an A operand that carries row i of k
+//     half kq/2 in A row i when kq is even and in A row 8 + i when kq is odd
+//     (zero otherwise) puts columns 0-15 of the block in D rows 0-7 and
+//     columns 16-31 in D rows 8-15.
+//   Direct (9-32 rows, or a K too long to stage): v_mfma_f32_32x32x16_f16 on
+//     the fragment as laid out, the A operand loaded from global memory with
+//     the weights (small and L2-resident; rows >= M are zero).
 template <int FORM> constexpr int gemv_depth() {
   return FORM == TGOHIP_FORM_I8 || FORM == TGOHIP_FORM_I4_TGO ? 2 : 4;
 }
-// Sixteen waves (1024 threads) where one column block per workgroup leaves
-// few workgroups and the form's registers allow it, eight otherwise.
-template <int FORM, int CB> constexpr int gemv_waves() {
-  return CB == 1 && (FORM == TGOHIP_FORM_I4_SYM || FORM == TGOHIP_FORM_I8) ? 16 : 8;
+// Waves per workgroup the registers allow (128 VGPRs at 16 waves): 16 for
+// one column block of the int4-sym and int8 packs, 8 otherwise.
+constexpr int gemv_max_waves(int form, int cb) {
+  return cb == 1 && (form == TGOHIP_FORM_I4_SYM || form == TGOHIP_FORM_I8) ? 16 : 8;
+}
+constexpr int kGemvStageBytes = (64 << 10) + 128;  // 8 rows of K = 4096, padded
+__host__ __device__ constexpr int gemv_stage_stride(int K) { return K + 8; }
+
+template <int EPI, int CB>
+__device__ __forceinline__ void gemv_store(const GemmArgs& g, int nbw0, const bool (&nbv)[CB], int row,
+                                           int col, const float (&v)[CB]) {
+  if constexpr (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+    if (!nbv[CB - 1]) return;
+    const float o = silu_f(v[0]) * v[CB - 1];
+    const size_t off = (size_t)row * (g.N / 2) + (nbw0 >> 1) * 32 + col;
+    if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[off] = (half_t)o;
+    else ((float*)g.y)[off] = o;
+  } else {
+#pragma unroll
+    for (int b = 0; b < CB; b++) {
+      if (!nbv[b]) continue;
+      const size_t off = (size_t)row * g.N + (nbw0 + b) * 32 + col;
+      if (EPI == EPI_F32) ((float*)g.y)[off] = v[b];
+      else if (EPI == EPI_F16) ((half_t*)g.y)[off] = (half_t)v[b];
+      else ((float*)g.y)[off] += v[b];
+    }
+  }
 }
 
-template <int FORM, int EPI, int CB>
-__global__ __launch_bounds__((64 * gemv_waves<FORM, CB>())) void gemm_gemv_kernel(GemmArgs g) {
+// STAGED: the staged 1-8 row form (dynamic LDS of M*K halves); else direct.
+template <int FORM, int EPI, int CB, int W, bool STAGED>
+__global__ __launch_bounds__(64 * W) void gemm_gemv_kernel(GemmArgs g) {
   constexpr int D = gemv_depth<FORM>();
-  constexpr int kGemvWaves = gemv_waves<FORM, CB>();
-  __shared__ float red[kGemvWaves][CB][32 * 32];
+  constexpr int ROWS = STAGED ? 8 : 32;
+  constexpr int OUT = CB * ROWS * 32;  // a wave's sums: CB blocks of ROWS rows x 32 columns
+  __shared__ float red[W][OUT];
+  extern __shared__ __attribute__((aligned(16))) half_t xs[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = lane >> 5, c32 = lane & 31;
   const int NBT = g.N / 32;
   const int nbw0 = blockIdx.x * CB;
   bool nbv[CB];
@@ -866,98 +907,195 @@ __global__ __launch_bounds__((64 * gemv_waves<FORM, CB>())) void gemm_gemv_kerne
     nbv[b] = nbw0 + b < NBT;
     nbl[b] = min(nbw0 + b, NBT - 1);
   }
-  const int per = (g.K / 64) / kGemvWaves, ks0 = wave * per;  // per % D == 0
-  const bool rv = c32 < g.M;
-  const half_t* xr = (const half_t*)g.x + (size_t)(rv ? c32 : 0) * g.K + 8 * h;
+  const int kw = (g.K / 64) / W, ks0 = wave * kw;  // kw % D == 0
+  // The lane's activation row and k half, and whether it carries one.
+  int arow, ah;
+  bool av;
+  if constexpr (STAGED) {
+    const int ai = lane & 15, kq = lane >> 4;
+    arow = ai & 7;
+    ah = kq >> 1;
+    av = ((ai < 8) == ((kq & 1) == 0)) && arow < g.M;
+  } else {
+    arow = lane & 31;
+    ah = lane >> 5;
+    av = arow < g.M;
+  }
+  const half_t* xr = (STAGED ? (const half_t*)xs : (const half_t*)g.x) +
+                     (size_t)(av ? arow : 0) * (STAGED ? gemv_stage_stride(g.K) : g.K) + 8 * ah;
 
-  float16_t acc[CB];
+  typedef typename std::conditional<STAGED, float4_t, float16_t>::type Acc;
+  Acc acc[CB];
 #pragma unroll
   for (int b = 0; b < CB; b++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[b][r] = 0.f;
+    for (int r = 0; r < (STAGED ? 4 : 16); r++) acc[b][r] = 0.f;
   BRaw<FORM> bq[D][CB];
   half8_t aq[D][4];
+  // A operand of k-step ks: from LDS (staged) or global memory, zero where the
+  // lane carries no row.
+  auto load_a = [&](half8_t(&a)[4], int ks) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if constexpr (STAGED) {
+        half8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (av) v = *(const half8_t*)(xr + ks * 64 + 16 * j);
+        a[j] = v;
+      } else {
+        const half8_t v = *(const half8_t*)(xr + ks * 64 + 16 * j);
+        a[j] = av ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+  };
   auto load = [&](int d, int ks) {
 #pragma unroll
     for (int b = 0; b < CB; b++) load_braw(g, nbl[b], ks, lane, bq[d][b]);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const half8_t v = *(const half8_t*)(xr + ks * 64 + 16 * j);
-      aq[d][j] = rv ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    if constexpr (!STAGED) load_a(aq[d], ks);
   };
 #pragma unroll
   for (int d = 0; d < D; d++) load(d, ks0 + d);
-  for (int i = 0; i < per; i += D) {
+  if constexpr (STAGED) {
+    const half_t* x = (const half_t*)g.x;
+    for (int i = tid * 8; i < g.M * g.K; i += 64 * W * 8) {
+      const int row = i / g.K;
+      *(half8_t*)(xs + row * gemv_stage_stride(g.K) + (i - row * g.K)) = *(const half8_t*)(x + i);
+    }
+    __syncthreads();
+  }
+  for (int i = 0; i < kw; i += D) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
+      if constexpr (STAGED) load_a(aq[d], ks0 + i + d);
 #pragma unroll
       for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int b = 0; b < CB; b++)
-          acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[d][j], bfrag(bq[d][b], j), acc[b], 0, 0, 0);
-      if (i + d + D < per) load(d, ks0 + i + d + D);
+        for (int b = 0; b < CB; b++) {
+          if constexpr (STAGED)
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[d][j], bfrag(bq[d][b], j), acc[b], 0, 0, 0);
+          else
+            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[d][j], bfrag(bq[d][b], j), acc[b], 0, 0, 0);
+        }
+      if (i + d + D < kw) load(d, ks0 + i + d + D);
     }
   }
-  // Lane (c32, h) holds D[8(r/4) + 4h + r%4][c32] of each block.
+  if constexpr (STAGED) {
+    // Lane l holds D[4(l/16) + r][l%16]: row 4((l/16)%2) + r of column l%16 + 16(l/32).
+    const int row0 = 4 * ((lane >> 4) & 1), col = (lane & 15) + 16 * (lane >> 5);
 #pragma unroll
-  for (int b = 0; b < CB; b++)
+    for (int b = 0; b < CB; b++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) red[wave][b][(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + c32] = acc[b][r];
+      for (int r = 0; r < 4; r++)
+        if (row0 + r < g.M) red[wave][b * 256 + (row0 + r) * 32 + col] = acc[b][r];
+  } else {
+    // Lane (c32, h) holds D[8(r/4) + 4h + r%4][c32] of each block.
+    const int h = lane >> 5, c32 = lane & 31;
+#pragma unroll
+    for (int b = 0; b < CB; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < g.M) red[wave][b * 1024 + row * 32 + c32] = acc[b][r];
+      }
+  }
   __syncthreads();
-  for (int idx = tid; idx < 32 * 32; idx += 64 * kGemvWaves) {
-    const int row = idx >> 5, col = idx & 31;
-    if (row >= g.M) continue;
+  for (int rc = tid; rc < g.M * 32; rc += 64 * W) {
     float v[CB];
 #pragma unroll
     for (int b = 0; b < CB; b++) {
       v[b] = 0.f;
 #pragma unroll
-      for (int w = 0; w < kGemvWaves; w++) v[b] += red[w][b][idx];
+      for (int w = 0; w < W; w++) v[b] += red[w][b * ROWS * 32 + rc];
     }
-    if constexpr (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
-      if (!nbv[CB - 1]) continue;
-      const float o = silu_f(v[0]) * v[CB - 1];
-      const size_t off = (size_t)row * (g.N / 2) + (nbw0 >> 1) * 32 + col;
-      if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[off] = (half_t)o;
-      else ((float*)g.y)[off] = o;
-    } else {
-#pragma unroll
-      for (int b = 0; b < CB; b++) {
-        if (!nbv[b]) continue;
-        const size_t off = (size_t)row * g.N + (nbw0 + b) * 32 + col;
-        if (EPI == EPI_F32) ((float*)g.y)[off] = v[b];
-        else if (EPI == EPI_F16) ((half_t*)g.y)[off] = (half_t)v[b];
-        else ((float*)g.y)[off] += v[b];
-      }
+    gemv_store<EPI, CB>(g, nbw0, nbv, rc >> 5, rc & 31, v);
+  }
+}
+
+// Launch shape of the small-M kernels: CB column blocks (2 for SwiGLU), the
+// form (staged or direct) and W waves per workgroup: the fewest of the
+// candidates (8, 16 staged; 4, 8, 16 direct) that put about three waves on
+// every SIMD (12 per CU), within the form's cap and with each wave's share of
+// K a whole multiple of the load depth; w = 0 when none fits. Measured at
+// M = 1: the staged LM head runs best at 8 waves (65 us; 66 at 4, 68 at 16),
+// QKV, O and down at 16.
+struct GemvShape {
+  int cb, w;
+  bool staged;
+};
+constexpr int kGemvWavesPerCU = 12;
+static GemvShape gemv_shape(const PackedWeight& w, int epi, int M, int ncu) {
+  GemvShape sh;
+  sh.cb = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? 2 : 1;
+  sh.staged = M <= 8 && (int64_t)M * gemv_stage_stride(w.K) * 2 <= kGemvStageBytes;
+  const int KS = w.K / 64, groups = (w.N / 32 + sh.cb - 1) / sh.cb;
+  const int D = (w.form == TGOHIP_FORM_I8 || w.form == TGOHIP_FORM_I4_TGO) ? 2 : 4;
+  sh.w = 0;
+  for (int c : {4, 8, 16}) {
+    if (sh.staged && c == 4) continue;
+    if (c > gemv_max_waves(w.form, sh.cb) || KS % (c * D) != 0) break;
+    sh.w = c;
+    if ((int64_t)groups * c >= (int64_t)kGemvWavesPerCU * ncu) break;
+  }
+  if (sh.w == 0 && KS % D == 0) {
+    sh.w = 1;
+    sh.staged = false;
+  }
+  return sh;
+}
+
+template <int FORM, int CB, int W, bool STAGED>
+static void launch_gemv_w(const GemmArgs& g, int epi, hipStream_t st) {
+  const dim3 grid((unsigned)((g.N / 32 + CB - 1) / CB)), blk(64 * W);
+  const size_t lds = STAGED ? (size_t)g.M * gemv_stage_stride(g.K) * 2 : 0;
+#define GEMV_LAUNCH(E, C)                                                                       \
+  do {                                                                                          \
+    if (STAGED) {                                                                               \
+      static const hipError_t attr = hipFuncSetAttribute(                                        \
+          (const void*)&gemm_gemv_kernel<FORM, E, C, W, STAGED>,                                 \
+          hipFuncAttributeMaxDynamicSharedMemorySize, kGemvStageBytes);                          \
+      (void)attr;                                                                               \
+    }                                                                                           \
+    hipLaunchKernelGGL((gemm_gemv_kernel<FORM, E, C, W, STAGED>), grid, blk, lds, st, g);      \
+  } while (0)
+  if constexpr (CB == 2) {
+    if (epi == EPI_SWIGLU_F16) GEMV_LAUNCH(EPI_SWIGLU_F16, 2);
+    else GEMV_LAUNCH(EPI_SWIGLU_F32, 2);
+  } else {
+    switch (epi) {
+      case EPI_F32: GEMV_LAUNCH(EPI_F32, 1); break;
+      case EPI_F16: GEMV_LAUNCH(EPI_F16, 1); break;
+      default: GEMV_LAUNCH(EPI_RESID, 1); break;
     }
+  }
+#undef GEMV_LAUNCH
+}
+
+template <int FORM, int CB, bool STAGED>
+static void launch_gemv_cb(const GemmArgs& g, int epi, int w, hipStream_t st) {
+  switch (w) {
+    case 1: launch_gemv_w<FORM, CB, 1, STAGED>(g, epi, st); break;
+    case 4: launch_gemv_w<FORM, CB, 4, STAGED>(g, epi, st); break;
+    case 8: launch_gemv_w<FORM, CB, 8, STAGED>(g, epi, st); break;
+    default:
+      if constexpr (gemv_max_waves(FORM, CB) >= 16) launch_gemv_w<FORM, CB, 16, STAGED>(g, epi, st);
+      break;
   }
 }
 
 template <int FORM>
-static void launch_gemv_form(const GemmArgs& g, int epi, hipStream_t st) {
-  const int NBT = g.N / 32;
-  const dim3 g1((unsigned)NBT), g2((unsigned)((NBT + 1) / 2));
-  const dim3 b1(64 * gemv_waves<FORM, 1>()), b2(64 * gemv_waves<FORM, 2>());
-  switch (epi) {
-    case EPI_F32: hipLaunchKernelGGL((gemm_gemv_kernel<FORM, EPI_F32, 1>), g1, b1, 0, st, g); break;
-    case EPI_F16: hipLaunchKernelGGL((gemm_gemv_kernel<FORM, EPI_F16, 1>), g1, b1, 0, st, g); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_gemv_kernel<FORM, EPI_RESID, 1>), g1, b1, 0, st, g); break;
-    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_gemv_kernel<FORM, EPI_SWIGLU_F16, 2>), g2, b2, 0, st, g); break;
-    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_gemv_kernel<FORM, EPI_SWIGLU_F32, 2>), g2, b2, 0, st, g); break;
+static void launch_gemv_form(const GemmArgs& g, int epi, const GemvShape& sh, hipStream_t st) {
+  if (sh.cb == 2) {
+    if (sh.staged) launch_gemv_cb<FORM, 2, true>(g, epi, sh.w, st);
+    else launch_gemv_cb<FORM, 2, false>(g, epi, sh.w, st);
+  } else {
+    if (sh.staged) launch_gemv_cb<FORM, 1, true>(g, epi, sh.w, st);
+    else launch_gemv_cb<FORM, 1, false>(g, epi, sh.w, st);
   }
 }
 
-// The small-M kernel serves f16 activations up to 32 rows when K divides
-// into equal, whole-depth shares for up to sixteen waves. For the int4 packs
-// a long K over few column blocks (the down projection) streams faster split
-// across workgroups by gemm_kernel (measured: 11.8 vs 12.5 us at K=12288,
-// N=4096, M=1).
-static bool use_gemv(const PackedWeight& w, bool x_f32, int M) {
-  const int KS = w.K / 64;
-  const bool int4 = w.form == TGOHIP_FORM_I4_SYM || w.form == TGOHIP_FORM_I4_TGO;
-  if (int4 && w.K > 8192 && w.N / 32 < 512) return false;
-  return !x_f32 && M <= 32 && KS % (16 * 4) == 0;
+// The small-M kernels serve f16 activations up to 32 rows when K's k-steps
+// divide into whole-depth shares.
+static bool use_gemv(const PackedWeight& w, bool x_f32, int M, int ncu) {
+  return !x_f32 && M <= 32 && gemv_shape(w, EPI_F32, M, ncu).w > 0;
 }
 
 // Split-K factor: enough workgroups to cover the chip twice, while each split
@@ -1144,7 +1282,7 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
     return fail(TGOHIP_ESTATE, "linear: only f32 and residual epilogues can defer split-K");
   if (use_pipe(w, x_f32, M))
     return gemm_pipe_enqueue(w, x, M, y, epi, workspace, ws_bytes, ncu, st, defer);
-  if (use_gemv(w, x_f32, M)) {
+  if (use_gemv(w, x_f32, M, ncu)) {
     GemmArgs g{};
     g.x = x;
     g.wp = w.wp;
@@ -1154,11 +1292,12 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
     g.M = M;
     g.K = w.K;
     g.N = w.N;
+    const GemvShape sh = gemv_shape(w, epi, M, ncu);
     switch (w.form) {
-      case TGOHIP_FORM_F16: launch_gemv_form<TGOHIP_FORM_F16>(g, epi, st); break;
-      case TGOHIP_FORM_I8: launch_gemv_form<TGOHIP_FORM_I8>(g, epi, st); break;
-      case TGOHIP_FORM_I4_TGO: launch_gemv_form<TGOHIP_FORM_I4_TGO>(g, epi, st); break;
-      case TGOHIP_FORM_I4_SYM: launch_gemv_form<TGOHIP_FORM_I4_SYM>(g, epi, st); break;
+      case TGOHIP_FORM_F16: launch_gemv_form<TGOHIP_FORM_F16>(g, epi, sh, st); break;
+      case TGOHIP_FORM_I8: launch_gemv_form<TGOHIP_FORM_I8>(g, epi, sh, st); break;
+      case TGOHIP_FORM_I4_TGO: launch_gemv_form<TGOHIP_FORM_I4_TGO>(g, epi, sh, st); break;
+      case TGOHIP_FORM_I4_SYM: launch_gemv_form<TGOHIP_FORM_I4_SYM>(g, epi, sh, st); break;
     }
     TGOHIP_HIP(hipGetLastError());
     return 0;
