@@ -955,10 +955,22 @@ __global__ __launch_bounds__(64 * W) void gemm_gemv_kernel(GemmArgs g) {
 #pragma unroll
   for (int d = 0; d < D; d++) load(d, ks0 + d);
   if constexpr (STAGED) {
+    // Every 16-byte chunk's load is issued before the first is written, so
+    // the copy costs one L2 round trip.
+    constexpr int SC = (kGemvStageBytes / 16 + 64 * W - 1) / (64 * W);
     const half_t* x = (const half_t*)g.x;
-    for (int i = tid * 8; i < g.M * g.K; i += 64 * W * 8) {
-      const int row = i / g.K;
-      *(half8_t*)(xs + row * gemv_stage_stride(g.K) + (i - row * g.K)) = *(const half8_t*)(x + i);
+    const int nch = g.M * g.K / 8;
+    half8_t t[SC];
+#pragma unroll
+    for (int u = 0; u < SC; u++)
+      if (tid + u * 64 * W < nch) t[u] = *(const half8_t*)(x + 8 * (tid + u * 64 * W));
+#pragma unroll
+    for (int u = 0; u < SC; u++) {
+      const int i = 8 * (tid + u * 64 * W);
+      if (i < 8 * nch) {
+        const int row = i / g.K;
+        *(half8_t*)(xs + row * gemv_stage_stride(g.K) + (i - row * g.K)) = t[u];
+      }
     }
     __syncthreads();
   }
@@ -1071,9 +1083,9 @@ static void launch_gemv_w(const GemmArgs& g, int epi, hipStream_t st) {
 
 template <int FORM, int CB, bool STAGED>
 static void launch_gemv_cb(const GemmArgs& g, int epi, int w, hipStream_t st) {
-  switch (w) {
-    case 1: launch_gemv_w<FORM, CB, 1, STAGED>(g, epi, st); break;
-    case 4: launch_gemv_w<FORM, CB, 4, STAGED>(g, epi, st); break;
+  switch (w) {  // the staged form runs 8 or 16 waves
+    case 1: if constexpr (!STAGED) launch_gemv_w<FORM, CB, 1, STAGED>(g, epi, st); break;
+    case 4: if constexpr (!STAGED) launch_gemv_w<FORM, CB, 4, STAGED>(g, epi, st); break;
     case 8: launch_gemv_w<FORM, CB, 8, STAGED>(g, epi, st); break;
     default:
       if constexpr (gemv_max_waves(FORM, CB) >= 16) launch_gemv_w<FORM, CB, 16, STAGED>(g, epi, st);
