@@ -488,7 +488,7 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
     doff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)(kc * 8)) * 2u;
   }
   const char* xa = (const char*)g.x;
-  PipeB<FORM> bq[4][2];  // B(k) in slot k % 4; three are live at a time
+  PipeB<FORM> bq[4][2];  // B(k) in slot k % 4, all four live
   // A wave's scales (lanes 0-15: blocks nbl[0], nbl[1]) and zeros (lanes
   // 16-31) of one k-step are 128-byte runs of the packed arrays.
   const int szl = lane & 15, szb = szl >> 3;
@@ -517,11 +517,13 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
 
   // A(k) (and the scales of B(k) when they travel by LDS) sits in LDS stage
   // k % 4, DMA'd in the middle of step k-3; B(k) in register slot k % 4,
-  // loaded at the start of step k-2. Each step reads the next step's first
+  // loaded at the start of step k-3 (the slot of B(k-4), whose last read
+  // was in step k-4; three steps ahead cut the M = 128 gate/up from 46 to
+  // 41 us). Each step reads the next step's first
   // fragments during its last substep, so the MFMAs run on across step
   // boundaries. One barrier per step, in its middle. Before it a wave waits
   // for its own DMA of stage k+1 (issued at step k-2: the vector memory
-  // operations issued since are B(k), stage k+2's DMA and B(k+1)) and for its
+  // operations issued since are B(k+2), stage k+2's DMA and B(k+3)) and for its
   // LDS reads; past it, stage k+1 is visible to every wave, and every wave is
   // done reading stage k-1, which the DMA of stage k+3 issued right after the
   // barrier reuses. The barrier carries no memory fence: a fence would wait
@@ -533,6 +535,8 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
     for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(0), lane, bq[0][b]);
 #pragma unroll
     for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(1), lane, bq[1][b]);
+#pragma unroll
+    for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(2), lane, bq[2][b]);
     PIPE_DMA_A(kpos(0), 0);
     PIPE_DMA_A(kpos(1), 1);
     PIPE_DMA_A(kpos(2), 2);
@@ -550,7 +554,7 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
 #pragma unroll
     for (int u = 0; u < 4; u++) {
 #pragma unroll
-      for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(kk + u + 2), lane, bq[(u + 2) % 4][b]);
+      for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(kk + u + 3), lane, bq[(u + 3) % 4][b]);
       // Keep the loads issued here, ahead of the MFMAs: the scheduler would
       // otherwise sink them next to their use and expose their latency.
       __builtin_amdgcn_sched_barrier(0);
