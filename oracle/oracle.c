@@ -428,47 +428,58 @@ void orc_ragged_attention_f64(const float* q, int T, int H, int Hkv, int dh,
   int group = H / Hkv;
   double bv = 0, bs = 0, bp = 0;
   memset(out, 0, sizeof(double) * (size_t)T * H * dh);
-  int tok = 0;
-  for (int s = 0; s < B; s++) {
-    int n = (int)extents[s], L = (int)lengths[s];
-    for (int i = 0; i < n; i++, tok++) {
-      if (tok >= T) break;
-      int limit = L - n + i;
+  /* token -> (sequence, index in its extent), in batch order */
+  int* tseq = (int*)malloc(sizeof(int) * (size_t)(T > 0 ? T : 1));
+  int* tidx = (int*)malloc(sizeof(int) * (size_t)(T > 0 ? T : 1));
+  int ntok = 0;
+  for (int s = 0; s < B && ntok < T; s++)
+    for (int i = 0; i < (int)extents[s] && ntok < T; i++, ntok++) {
+      tseq[ntok] = s;
+      tidx[ntok] = i;
+    }
+  /* Rows and heads are independent; each (row, head) sums its positions in
+   * ascending order exactly as a serial walk would. */
+#pragma omp parallel for schedule(dynamic, 1) collapse(2) reduction(max : bv, bs, bp)
+  for (int tok = 0; tok < ntok; tok++) {
+    for (int h = 0; h < H; h++) {
+      int s = tseq[tok], n = (int)extents[s], L = (int)lengths[s];
+      int limit = L - n + tidx[tok];
+      int kvh = h / group;
       double* scores = (double*)malloc(sizeof(double) * (size_t)(limit + 1));
-      for (int h = 0; h < H; h++) {
-        int kvh = h / group;
-        double mx = -INFINITY;
-        for (int p = 0; p <= limit; p++) {
-          size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
-          double dot = 0;
-          for (int d = 0; d < dh; d++) {
-            double qv = q[((size_t)tok * H + h) * dh + d];
-            size_t ki = (row * Hkv + kvh) * dh + d;
-            double kv = k_f16 ? orc_f16_to_f32(k_f16[ki]) : k_f32[ki];
-            dot += qv * kv;
-          }
-          scores[p] = dot * scale;
-          if (scores[p] > mx) mx = scores[p];
-          if (fabs(scores[p]) > bs) bs = fabs(scores[p]);
-        }
-        if (limit + 1 > bp) bp = limit + 1;
-        double sum = 0;
-        for (int p = 0; p <= limit; p++) { scores[p] = exp(scores[p] - mx); sum += scores[p]; }
+      double* acc = (double*)calloc((size_t)dh, sizeof(double));
+      double mx = -INFINITY;
+      for (int p = 0; p <= limit; p++) {
+        size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+        double dot = 0;
         for (int d = 0; d < dh; d++) {
-          double acc = 0;
-          for (int p = 0; p <= limit; p++) {
-            size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
-            size_t vi = (row * Hkv + kvh) * dh + d;
-            double val = v_f16 ? orc_f16_to_f32(v_f16[vi]) : v_f32[vi];
-            acc += scores[p] * val;
-            if (fabs(val) > bv) bv = fabs(val);
-          }
-          out[((size_t)tok * H + h) * dh + d] = acc / sum;
+          double qv = q[((size_t)tok * H + h) * dh + d];
+          size_t ki = (row * Hkv + kvh) * dh + d;
+          double kv = k_f16 ? orc_f16_to_f32(k_f16[ki]) : k_f32[ki];
+          dot += qv * kv;
+        }
+        scores[p] = dot * scale;
+        if (scores[p] > mx) mx = scores[p];
+        if (fabs(scores[p]) > bs) bs = fabs(scores[p]);
+      }
+      if (limit + 1 > bp) bp = limit + 1;
+      double sum = 0;
+      for (int p = 0; p <= limit; p++) { scores[p] = exp(scores[p] - mx); sum += scores[p]; }
+      for (int p = 0; p <= limit; p++) {
+        size_t row = (size_t)pages[(size_t)s * max_pages + p / block] * block + p % block;
+        for (int d = 0; d < dh; d++) {
+          size_t vi = (row * Hkv + kvh) * dh + d;
+          double val = v_f16 ? orc_f16_to_f32(v_f16[vi]) : v_f32[vi];
+          acc[d] += scores[p] * val;
+          if (fabs(val) > bv) bv = fabs(val);
         }
       }
+      for (int d = 0; d < dh; d++) out[((size_t)tok * H + h) * dh + d] = acc[d] / sum;
+      free(acc);
       free(scores);
     }
   }
+  free(tseq);
+  free(tidx);
   if (budget3) { budget3[0] = bv; budget3[1] = bs; budget3[2] = bp; }
 }
 
