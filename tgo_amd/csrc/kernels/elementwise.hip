@@ -49,6 +49,40 @@ __global__ void embed_kernel(const uint32_t* ids, const void* table, const uint1
 // With nsplit > 0 the residual add of a split-K projection is still pending:
 // x[src, :] += sum_s part[s][src, :] (summed in split order, as
 // gemm_reduce_kernel would) is done here first and written back to x.
+// acc += the N planes at p, p + plane, ... (element offset off), added in
+// plane order after all N loads are issued.
+template <int N>
+__device__ __forceinline__ void add_planes(float4_t& acc, const float* p, size_t plane, size_t off) {
+  float4_t v[N];
+#pragma unroll
+  for (int u = 0; u < N; u++) v[u] = *(const float4_t*)(p + (size_t)u * plane + off);
+#pragma unroll
+  for (int u = 0; u < N; u++) acc += v[u];
+}
+
+// Sum of nsplit split-K partial planes at element offset off, in split order
+// (the order gemm_reduce_kernel adds them). Up to eight planes' loads are in
+// flight together; a loop of load-then-add waited for each in turn (8 round
+// trips for the 8-split projections of a 128-row step).
+__device__ __forceinline__ float4_t sum_planes(const float* part, int nsplit, size_t plane,
+                                               size_t off) {
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    const float* p = part + (size_t)s0 * plane;
+    switch (min(nsplit - s0, 8)) {
+      case 1: add_planes<1>(acc, p, plane, off); break;
+      case 2: add_planes<2>(acc, p, plane, off); break;
+      case 3: add_planes<3>(acc, p, plane, off); break;
+      case 4: add_planes<4>(acc, p, plane, off); break;
+      case 5: add_planes<5>(acc, p, plane, off); break;
+      case 6: add_planes<6>(acc, p, plane, off); break;
+      case 7: add_planes<7>(acc, p, plane, off); break;
+      default: add_planes<8>(acc, p, plane, off); break;
+    }
+  }
+  return acc;
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -72,9 +106,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t*
   for (int i = threadIdx.x * 4; i < w; i += step) {
     float4_t v = *(const float4_t*)(x + src + i);
     if (nsplit > 0) {
-      float4_t acc = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < nsplit; sp++) acc += *(const float4_t*)(part + sp * plane + src + i);
-      v += acc;
+      v += sum_planes(part, nsplit, plane, src + i);
       *(float4_t*)(x + src + i) = v;
     }
     ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
@@ -154,8 +186,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
     if (a.nsplit == 0) {
       v = *(const float4_t*)(a.qkv + off);
     } else {
-      v = float4_t{0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < a.nsplit; sp++) v += *(const float4_t*)(a.qkv + sp * a.plane + off);
+      v = sum_planes(a.qkv, a.nsplit, a.plane, off);
     }
     if (hh >= a.H + a.Hkv) {
       // value head: narrowed and scattered as is
@@ -240,7 +271,19 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V
   const int V4 = V / 4;
   const float4_t* row4 = (const float4_t*)row;  // rows are 16-byte aligned when V % 4 == 0
   if ((V & 3) == 0) {
-    for (int i4 = t; i4 < V4; i4 += 1024) {
+    // Eight float4 loads in flight per thread (a loop of load-then-compare
+    // waited for each); the thread still visits its elements in ascending order.
+    int i4 = t;
+    for (; i4 + 7 * 1024 < V4; i4 += 8 * 1024) {
+      float4_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = row4[i4 + u * 1024];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) take(v[u][j], 4 * (i4 + u * 1024) + j);
+    }
+    for (; i4 < V4; i4 += 1024) {
       const float4_t v = row4[i4];
 #pragma unroll
       for (int j = 0; j < 4; j++) take(v[j], 4 * i4 + j);

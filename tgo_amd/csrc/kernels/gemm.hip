@@ -619,6 +619,36 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
 #undef PIPE_DMA_A
 }
 
+// a += p[0], p[plane], ... p[(N-1) plane] in that order, every load issued
+// before the first add.
+template <int N>
+__device__ __forceinline__ void add_split_values(float& a, const float* p, size_t plane) {
+  float v[N];
+#pragma unroll
+  for (int u = 0; u < N; u++) v[u] = p[(size_t)u * plane];
+#pragma unroll
+  for (int u = 0; u < N; u++) a += v[u];
+}
+// Sum of the split partials at p (planes `plane` apart), in split order, up
+// to eight loads in flight at a time.
+__device__ __forceinline__ float sum_split_values(const float* p, int splits, size_t plane) {
+  float a = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    const float* q = p + (size_t)s0 * plane;
+    switch (min(splits - s0, 8)) {
+      case 1: add_split_values<1>(a, q, plane); break;
+      case 2: add_split_values<2>(a, q, plane); break;
+      case 3: add_split_values<3>(a, q, plane); break;
+      case 4: add_split_values<4>(a, q, plane); break;
+      case 5: add_split_values<5>(a, q, plane); break;
+      case 6: add_split_values<6>(a, q, plane); break;
+      case 7: add_split_values<7>(a, q, plane); break;
+      default: add_split_values<8>(a, q, plane); break;
+    }
+  }
+  return a;
+}
+
 // Sums split-K partials in split order and applies the epilogue.
 template <int EPI>
 __global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
@@ -629,17 +659,13 @@ __global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
   const size_t plane = g.pstride;
   if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
     const int gc = (col / 32) * 64 + (col % 32), uc = gc + 32;
-    float ga = 0.f, ua = 0.f;
-    for (int s = 0; s < splits; s++) {
-      ga += g.part[s * plane + (size_t)row * g.N + gc];
-      ua += g.part[s * plane + (size_t)row * g.N + uc];
-    }
+    const float ga = sum_split_values(g.part + (size_t)row * g.N + gc, splits, plane);
+    const float ua = sum_split_values(g.part + (size_t)row * g.N + uc, splits, plane);
     const float v = silu_f(ga) * ua;
     if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[i] = (half_t)v;
     else ((float*)g.y)[i] = v;
   } else {
-    float a = 0.f;
-    for (int s = 0; s < splits; s++) a += g.part[s * plane + i];
+    const float a = sum_split_values(g.part + i, splits, plane);
     if (EPI == EPI_F32) ((float*)g.y)[i] = a;
     else if (EPI == EPI_F16) ((half_t*)g.y)[i] = (half_t)a;
     else ((float*)g.y)[i] += a;
