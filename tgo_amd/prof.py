@@ -12,6 +12,10 @@
         GRBM_GUI_ACTIVE is the sum over the 8 XCDs, each counting the dispatch's cycles,
         which its ratio to the duration shows), from one rocprofv3 --pmc pass over those
         three counters.
+    python -m tgo_amd.prof grids <dir>/<name>_kernel_trace.csv
+        per (kernel, grid size): dispatches and the median and mean duration, so
+        launches of one kernel at different shapes stay apart (from --kernel-trace
+        --output-format csv).
     python -m tgo_amd.prof pmc <fetch_counter_collection.csv> <write_counter_collection.csv>
         per-kernel mean FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by
         what the same counter reads for the copy-probe dispatch (torch.neg over a
@@ -37,6 +41,20 @@ def stats(path):
         print("%-52s %7d %12.3f %11.2f %6.2f" % (
             short(r["Name"])[:52], int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6,
             float(r["AverageNs"]) / 1e3, 100 * float(r["TotalDurationNs"]) / tot))
+
+
+def grids(path):
+    agg = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) *
+               int(r["Grid_Size_Z"]), int(r["Workgroup_Size_X"]))
+        agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("%-52s %10s %6s %7s %10s %10s" % ("kernel", "threads", "wg", "disp", "median_us",
+                                           "mean_us"))
+    for (name, grid, wg), d in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        d = sorted(d)
+        print("%-52s %10d %6d %7d %10.2f %10.2f" % (name[:52], grid, wg, len(d), d[len(d) // 2],
+                                                   sum(d) / len(d)))
 
 
 def pmc(fetch_path, write_path, probe_mib):
@@ -145,6 +163,8 @@ def mfma(path, label):
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2])
+    elif sys.argv[1] == "grids":
+        grids(sys.argv[2])
     elif sys.argv[1] == "mfma":
         mfma(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "pmc":
