@@ -424,7 +424,8 @@ __device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I8>& r, in
 // NW waves (4 or 8) side by side in N: a workgroup owns MW rows x 64*NW columns.
 template <int FORM, int EPI, int MW, int NW>
 __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs g, int tiles_n,
-                                                                       int tiles, int colmajor) {
+                                                                       int tiles, int colmajor,
+                                                                       int xsplit) {
   constexpr int MB = MW / 32;
   constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step
   // Four LDS stages, separate arrays so the compiler can tell a DMA into one
@@ -448,19 +449,30 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
   // tile there. Within an XCD the order is row-major over its columns (the
   // workgroups in flight share a row tile of activations), or with colmajor
   // column-major (they share a column tile of weights: its row tiles run side
-  // by side and read it from HBM once).
+  // by side and read it from HBM once). With xsplit (2, 4 or 8) split-K
+  // slices the XCDs instead of riding grid.z: XCD x takes split x / G
+  // (G = 8 / xsplit) and, of that split, the column tiles c = x % G (mod G),
+  // so each XCD reads only its split's share of the activations (with 8
+  // splits a 128-row step's activations cross into the L2s once, not 8 times).
   const int x = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
-  const int cols_x = (tiles_n - x + 7) / 8;
+  int G = 8, r = x, split = (int)blockIdx.z, nsplit = (int)gridDim.z;
+  if (xsplit > 1) {
+    G = 8 / xsplit;
+    split = x / G;
+    r = x - split * G;
+    nsplit = xsplit;
+  }
+  const int cols_x = (tiles_n - r + G - 1) / G;
   const int rows_t = tiles / tiles_n;
   if (cols_x <= 0 || j >= cols_x * rows_t) return;
   int tm, tn;
   if (colmajor) {
     const int cj = j / rows_t;
     tm = j - cj * rows_t;
-    tn = x + 8 * cj;
+    tn = r + G * cj;
   } else {
     tm = j / cols_x;
-    tn = x + 8 * (j - tm * cols_x);
+    tn = r + G * (j - tm * cols_x);
   }
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -470,7 +482,7 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
   const int nbw0 = tn * 2 * NW + wave * 2;
   const int m0 = tm * MW;
   const int KS = g.K / 64;
-  const int ks0 = blockIdx.z * g.ksteps_per_split;
+  const int ks0 = split * g.ksteps_per_split;
   const int nk = min(KS, ks0 + g.ksteps_per_split) - ks0;
   const bool nbv[2] = {nbw0 < NBT, nbw0 + 1 < NBT};
   // Out-of-range column blocks load a valid block (results are not stored).
@@ -615,7 +627,7 @@ __global__ __launch_bounds__((64 * NW), (8 / NW)) void gemm_pipe_kernel(GemmArgs
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // no DMA into LDS outlives the loop
-  gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, gridDim.z > 1, blockIdx.z);
+  gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, nsplit > 1, split);
 #undef PIPE_DMA_A
 }
 
@@ -1234,23 +1246,23 @@ size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
 
 template <int FORM, int MW, int NW>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
-                             int cm, hipStream_t st) {
+                             int cm, int xs, hipStream_t st) {
   const dim3 blk(64 * NW);
   switch (epi) {
-    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm); break;
-    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm); break;
-    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm); break;
-    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm); break;
+    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
+    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
+    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW, NW>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
   }
 }
 
 template <int FORM>
 static void launch_pipe_shape(const GemmArgs& g, int epi, dim3 grid, int mw, int nw, int tiles_n,
-                              int tiles, int cm, hipStream_t st) {
-  if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, cm, st);
-  else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, cm, st);
-  else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, cm, st);
+                              int tiles, int cm, int xs, hipStream_t st) {
+  if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+  else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+  else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
 }
 
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
@@ -1276,20 +1288,24 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
     g.part = workspace;
     g.pstride = split_plane_stride(M, w.N);
   }
-  const dim3 grid((unsigned)(8 * ((tiles_n + 7) / 8) * (tiles / tiles_n)), 1, (unsigned)splits);
+  // 2, 4 or 8 splits slice the XCDs (see the kernel), others ride grid.z.
+  const int xs = (splits == 2 || splits == 4 || splits == 8) ? splits : 0;
+  const int G = xs ? 8 / xs : 8;
+  const dim3 grid((unsigned)(8 * ((tiles_n + G - 1) / G) * (tiles / tiles_n)), 1,
+                  (unsigned)(xs ? 1 : splits));
   // Few row tiles (at most 4: the LM head at a batch's 130-odd rows): the row
   // tiles of a column tile run side by side and read its weights once
   // (262 -> 250 us for the C4 LM head at 136 rows).
   const int cm = tiles / tiles_n <= 4 ? 1 : 0;
   switch (w.form) {
     case TGOHIP_FORM_I4_SYM:
-      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, tiles_n, tiles, cm, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, tiles_n, tiles, cm, xs, st);
       break;
     case TGOHIP_FORM_I4_TGO:
-      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, tiles_n, tiles, cm, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, tiles_n, tiles, cm, xs, st);
       break;
     default:
-      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, tiles_n, tiles, cm, st);
+      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, tiles_n, tiles, cm, xs, st);
       break;
   }
   if (defer) *defer = splits > 1 ? splits : 0;

@@ -16,6 +16,10 @@
         per (kernel, grid size): dispatches and the median and mean duration, so
         launches of one kernel at different shapes stay apart (from --kernel-trace
         --output-format csv).
+    python -m tgo_amd.prof pmcproj <fetch_counter_collection.csv> <write_counter_collection.csv> [probe_mib]
+        the same scaled FETCH_SIZE / WRITE_SIZE per projection of the step (labelled as
+        by mfma), with the fetch over the projection's int4-sym weight bytes at the C4
+        (Qwen3-8B) shapes.
     python -m tgo_amd.prof pmc <fetch_counter_collection.csv> <write_counter_collection.csv>
         per-kernel mean FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by
         what the same counter reads for the copy-probe dispatch (torch.neg over a
@@ -85,6 +89,42 @@ def pmc(fetch_path, write_path, probe_mib):
         if n.startswith("tgohip::attn_kernel"):
             attn = (fm + wm) * 1e6
     print("traffic_bytes_per_launch attn_kernel: %.0f" % attn)
+
+
+# int4-sym weight + scale bytes of the C4 (Qwen3-8B) projections: K*N*(0.5 + 2/32)
+C4_WEIGHT_BYTES = {"qkv": 4096 * 6144 * 0.5625, "o": 4096 * 4096 * 0.5625,
+                   "gateup": 4096 * 24576 * 0.5625, "down": 12288 * 4096 * 0.5625,
+                   "lm_head": 4096 * 151936 * 0.5625}
+
+
+def pmcproj(fetch_path, write_path, probe_mib):
+    probe = "copy-probe (torch.neg f32)"
+    known_kib = probe_mib * 1024.0
+    res = {}
+    for path, counter in ((fetch_path, "FETCH_SIZE"), (write_path, "WRITE_SIZE")):
+        per = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                d = per.setdefault(int(r["Dispatch_Id"]), {"name": short(r["Kernel_Name"]), "v": 0.0})
+                d["v"] += float(r["Counter_Value"])
+        ids = sorted(per)
+        names = [per[i]["name"] for i in ids]
+        scale = known_kib / next(per[i]["v"] for i in ids if per[i]["name"] == probe)
+        agg = collections.defaultdict(list)
+        for i, lab in zip(ids, label_projections(names)):
+            if lab:
+                agg[lab].append(per[i]["v"] * scale * 1024)
+        res[counter] = agg
+    print("%-8s %6s %12s %12s %14s %12s" % ("proj", "disp", "fetch_MB", "write_MB", "weights_MB",
+                                             "fetch/wts"))
+    for lab in ("qkv", "o", "gateup", "down", "lm_head"):
+        f = res["FETCH_SIZE"].get(lab)
+        w = res["WRITE_SIZE"].get(lab)
+        if not f or not w:
+            continue
+        fm, wm = sum(f) / len(f) / 1e6, sum(w) / len(w) / 1e6
+        wb = C4_WEIGHT_BYTES[lab] / 1e6
+        print("%-8s %6d %12.2f %12.2f %14.2f %12.3f" % (lab, len(f), fm, wm, wb, fm / wb))
 
 
 MFMA_PEAK_TFLOPS = 2500.0
@@ -167,6 +207,8 @@ if __name__ == "__main__":
         grids(sys.argv[2])
     elif sys.argv[1] == "mfma":
         mfma(sys.argv[2], sys.argv[3])
+    elif sys.argv[1] == "pmcproj":
+        pmcproj(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
     elif sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
     else:
