@@ -114,6 +114,20 @@ def copy_probe(mib):
     torch.cuda.empty_cache()
 
 
+def achievable_peaks(ctx):
+    """What this box reaches, measured before the timed work, beside the published peaks:
+    the library's streaming read of 2 GiB and its dense f16 MFMA loop (tgohip_probe_peaks,
+    medians of 5 timed launches)."""
+    read_gbps, mfma_tflops = ctx.probe_peaks(2 << 30, 5)
+    return {
+        "read_gbps": round(read_gbps, 1),
+        "mfma_f16_tflops": round(mfma_tflops, 1),
+        "how": "tgohip_probe_peaks before the timed region: a grid-stride read of 2 GiB "
+               "(16-byte loads) and independent v_mfma_f32_32x32x16_f16 chains on every CU; "
+               "medians of 5",
+    }
+
+
 class Workload:
     """Seeded arrivals and completions driving the library's Scheduler so that
     every step carries 128 decodes and 2 prefill chunks of 512.
@@ -516,6 +530,8 @@ def main():
         return
     t_setup = time.perf_counter()
     ctx = tgo_amd.Context(0)
+    # the box's achievable peaks, before any pool or weight is allocated
+    ach = achievable_peaks(ctx) if args.phase == "both" else None
     ctx.set_precision(args.precision)
     ctx.config(C4["layers"], C4["hidden"], C4["heads"], C4["kv_heads"], C4["head_dim"],
                C4["ffn"], C4["vocab"], C4["rms_eps"], C4["rope_theta"], C4["block"])
@@ -599,6 +615,11 @@ def main():
         "mfma_counters": recorded_mfma(),
     }
     ctx.close()
+    if ach:
+        result["achievable"] = ach
+        result["roofline"]["frac_of_achievable_read"] = round(achieved / ach["read_gbps"], 4)
+        if decode:
+            decode["hbm_frac_of_achievable_read"] = round(decode["hbm_gbps"] / ach["read_gbps"], 4)
     if not args.no_cpu:
         cb = cpu_baseline(last_st, last_pages, maxp, last_out, args.form)
         cb.pop("seconds")

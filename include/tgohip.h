@@ -380,6 +380,14 @@ enum {
 int tgohip_set_profile_kernels(tgohip_ctx* ctx, int stride, int mask);
 int tgohip_profile_read_kernel(tgohip_ctx* ctx, int kind, double* ms, double* bytes,
                                double* flops, int64_t* launches);
+/* What this box reaches (measurement helper, no counterpart in the reference;
+ * the benchmark reports it beside the published peaks): a streaming read of
+ * read_bytes (16-byte loads, grid-stride; a buffer the call allocates, fills
+ * and frees) and a dense f16 MFMA loop (independent v_mfma_f32_32x32x16_f16
+ * chains, four waves per workgroup, four workgroups per CU); medians of reps
+ * timed launches on the context's stream. */
+int tgohip_probe_peaks(tgohip_ctx* ctx, size_t read_bytes, int reps, double* read_gbps,
+                       double* mfma_tflops);
 /* Fills positions [0, positions) of every layer's K and V with seeded f16
  * N(0,1)*sigma: the context of sequences admitted already prefilled. */
 int tgohip_kv_synth(tgohip_ctx* ctx, uint64_t seed, double sigma, int positions);

@@ -125,6 +125,7 @@ def lib():
         "tgohip_set_profile_kernels": (I, [P, I, I]),
         "tgohip_profile_read_kernel": (I, [P, I, P, P, P, P]),
         "tgohip_kv_synth": (I, [P, U64, D, I]),
+        "tgohip_probe_peaks": (I, [P, ctypes.c_size_t, I, P, P]),
         "tgohip_to_f16": (ctypes.c_size_t, [P, P, ctypes.c_size_t]),
         "tgohip_quantize_int8": (None, [P, ctypes.c_size_t, P, P]),
         "tgohip_quantize_int4": (None, [P, ctypes.c_size_t, P, P, P]),
@@ -486,6 +487,13 @@ class Context:
 
     def kv_synth(self, seed, sigma, positions):
         check(lib().tgohip_kv_synth(self.h, seed, sigma, positions))
+
+    def probe_peaks(self, read_bytes=2 << 30, reps=5):
+        """(read GB/s, dense f16 MFMA TFLOP/s) this box reaches: tgohip_probe_peaks."""
+        gbps, tflops = ctypes.c_double(), ctypes.c_double()
+        check(lib().tgohip_probe_peaks(self.h, read_bytes, reps, ctypes.byref(gbps),
+                                       ctypes.byref(tflops)))
+        return gbps.value, tflops.value
 
     def set_profile(self, on, stride=1):
         """Time the attention launch of every `stride`-th layer (HIP events)."""

@@ -13,7 +13,7 @@ LIB = os.path.join(HERE, "libtgohip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_SOURCES = ["runtime.hip", "kernels/attention.hip", "kernels/gemm.hip",
-               "kernels/elementwise.hip"]
+               "kernels/elementwise.hip", "kernels/probe.hip"]
 CXX_SOURCES = ["host/hostlogic.cpp", "host/checkpoint.cpp"]
 
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",

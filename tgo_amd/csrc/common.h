@@ -188,4 +188,8 @@ void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipS
 void launch_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out, hipStream_t st);
 void launch_fill_f32(float* p, size_t n, float v, hipStream_t st);
 
+// ---- peak probes (kernels/probe.hip) ---------------------------------------
+int probe_read_enqueue(const void* p, size_t bytes, uint32_t* sink, hipStream_t st);
+double probe_mfma_enqueue(int blocks, int iters, float* sink, hipStream_t st);
+
 }  // namespace tgohip

@@ -1812,6 +1812,62 @@ int tgohip_profile_read(tgohip_ctx* c, double* attn_ms, double* attn_bytes, int6
   return tgohip_profile_read_kernel(c, TGOHIP_PROF_ATTN, attn_ms, attn_bytes, &flops, launches);
 }
 
+// The box's achievable peaks: a streaming read of read_bytes (a buffer this
+// call allocates, fills and frees) and a dense f16 MFMA loop over every CU;
+// medians of reps timed launches on the context's stream, after one untimed.
+int tgohip_probe_peaks(tgohip_ctx* c, size_t read_bytes, int reps, double* read_gbps,
+                       double* mfma_tflops) {
+  if (read_bytes < ((size_t)1 << 20) || reps < 1)
+    return fail(TGOHIP_EINVAL, "probe_peaks: read_bytes " + std::to_string(read_bytes) +
+                                   " (at least 1 MiB) and reps " + std::to_string(reps) +
+                                   " (at least 1)");
+  read_bytes &= ~(size_t)15;
+  void* buf = nullptr;
+  void* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  std::vector<float> rt, mt;
+  double flops = 0;
+  int rc = 0;
+  auto cleanup = [&] {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (buf) (void)hipFree(buf);
+    if (sink) (void)hipFree(sink);
+  };
+  if (hipMalloc(&buf, read_bytes) != hipSuccess || hipMalloc(&sink, 256) != hipSuccess ||
+      hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    cleanup();
+    return fail(TGOHIP_ENOMEM, "probe_peaks: " + std::to_string(read_bytes) + " bytes");
+  }
+  auto timed = [&](auto launch, std::vector<float>& out) -> int {
+    for (int i = 0; i <= reps; i++) {
+      if (hipEventRecord(e0, c->stream) != hipSuccess) return fail(TGOHIP_EDEVICE, "probe: event");
+      int r = launch();
+      if (r) return r;
+      if (hipEventRecord(e1, c->stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
+        return fail(TGOHIP_EDEVICE, "probe: event");
+      float ms = 0;
+      if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return fail(TGOHIP_EDEVICE, "probe: timing");
+      if (i > 0) out.push_back(ms);
+    }
+    std::sort(out.begin(), out.end());
+    return 0;
+  };
+  if (hipMemsetAsync(buf, 0x5a, read_bytes, c->stream) != hipSuccess) rc = fail(TGOHIP_EDEVICE, "probe: fill");
+  if (!rc)
+    rc = timed([&] { return probe_read_enqueue(buf, read_bytes, (uint32_t*)sink, c->stream); }, rt);
+  if (!rc)
+    rc = timed([&] {
+      flops = probe_mfma_enqueue(4 * c->ncu, 2048, (float*)sink, c->stream);
+      return (int)(hipGetLastError() != hipSuccess ? fail(TGOHIP_EDEVICE, "probe: mfma launch") : 0);
+    }, mt);
+  cleanup();
+  if (rc) return rc;
+  *read_gbps = read_bytes / (rt[rt.size() / 2] * 1e-3) / 1e9;
+  *mfma_tflops = flops / (mt[mt.size() / 2] * 1e-3) / 1e12;
+  return 0;
+}
+
 // Fills positions [0, positions) of every layer of the K and V pools with
 // loader-rule f16 of N(0,1)*sigma from (seed, stream 0x4b / 0x56): the synthetic
 // context of sequences admitted already prefilled.
