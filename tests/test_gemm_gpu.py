@@ -67,7 +67,7 @@ def test_dequant_is_bit_exact(ctx, torch_gpu, form):
 
 
 @pytest.mark.parametrize("form", [0, 1, 2, 3])
-@pytest.mark.parametrize("M", [1, 8, 33, 64, 130, 300])
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 33, 64, 130, 300])
 @pytest.mark.parametrize("xf32", [True, False])
 def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xf32):
     torch = torch_gpu
@@ -152,6 +152,40 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
             assert bool(((y[:, cols].double() - ref).abs() <= tol).all()), M
     finally:
         ctx.weight_free(h)
+
+
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [1, 5, 8, 9, 32])
+def test_small_m_forms_against_the_oracle(ctx, torch_gpu, form, M):
+    """Every weight form through the small-M kernels at K = 2048 (the staged form at 1-8
+    rows, direct at 9-32), f16 activations, against the float64 product of the same
+    operands and against tgo's CPU path (f32 activations, unrounded weights)."""
+    torch = torch_gpu
+    import tgo_amd
+    rng = np.random.default_rng(500 + form * 11 + M)
+    K, N = 2048, 512 if form != 2 else 640
+    wd, _ = make_weight(form, K, N, rng)
+    w32 = deq(form, K, N, wd)
+    w16 = w32.astype(np.float16).astype(np.float64)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    try:
+        dx = torch.from_numpy(x.astype(np.float16)).cuda()
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.linear(h, dx, M, y, x_dtype=tgo_amd.F16)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().astype(np.float64)
+    finally:
+        ctx.weight_free(h)
+    xu = x.astype(np.float16).astype(np.float64)
+    ref = xu @ w16
+    mag = np.abs(xu) @ np.abs(w16)
+    tol = 4 * np.sqrt(K) * 2.0 ** -24 * mag + 1e-30
+    assert np.all(np.abs(got - ref) <= tol), np.max(np.abs(got - ref) / tol)
+    cpu = oracle.cpu_linear(x, form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    mag2 = np.abs(x.astype(np.float64)) @ np.abs(w32.astype(np.float64))
+    tol2 = (2.0 ** -11 * 2 + 8 * np.sqrt(K) * 2.0 ** -24) * mag2
+    assert np.all(np.abs(got - cpu) <= tol2)
 
 
 @pytest.mark.parametrize("KN", [(4096, 6144), (12288, 4096), (4096, 24576), (4096, 151936)])

@@ -1079,20 +1079,26 @@ constexpr int kGemvWavesPerCU = 12;
 static GemvShape gemv_shape(const PackedWeight& w, int epi, int M, int ncu) {
   GemvShape sh;
   sh.cb = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? 2 : 1;
-  sh.staged = M <= 8 && (int64_t)M * gemv_stage_stride(w.K) * 2 <= kGemvStageBytes;
   const int KS = w.K / 64, groups = (w.N / 32 + sh.cb - 1) / sh.cb;
   const int D = (w.form == TGOHIP_FORM_I8 || w.form == TGOHIP_FORM_I4_TGO) ? 2 : 4;
-  sh.w = 0;
-  for (int c : {4, 8, 16}) {
-    if (sh.staged && c == 4) continue;
-    if (c > gemv_max_waves(w.form, sh.cb) || KS % (c * D) != 0) break;
-    sh.w = c;
-    if ((int64_t)groups * c >= (int64_t)kGemvWavesPerCU * ncu) break;
-  }
-  if (sh.w == 0 && KS % D == 0) {
-    sh.w = 1;
+  auto pick = [&](bool staged) {
+    int wv = 0;
+    for (int c : {4, 8, 16}) {
+      if (staged && c == 4) continue;
+      if (c > gemv_max_waves(w.form, sh.cb) || KS % (c * D) != 0) break;
+      wv = c;
+      if ((int64_t)groups * c >= (int64_t)kGemvWavesPerCU * ncu) break;
+    }
+    return wv;
+  };
+  // Staged when the rows fit and a staged wave count divides K; else direct.
+  sh.staged = M <= 8 && (int64_t)M * gemv_stage_stride(w.K) * 2 <= kGemvStageBytes;
+  sh.w = sh.staged ? pick(true) : 0;
+  if (sh.w == 0) {
     sh.staged = false;
+    sh.w = pick(false);
   }
+  if (sh.w == 0 && KS % D == 0) sh.w = 1;
   return sh;
 }
 
