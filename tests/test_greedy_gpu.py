@@ -104,6 +104,38 @@ def test_vocabulary_rows_with_the_maximum_everywhere(ctx, torch_gpu):
     assert mg[-1] == 2.0 ** -20
 
 
+@pytest.mark.parametrize("B", [1, 33, 100, 130, 600])
+def test_batches_of_vocabulary_rows(ctx, torch_gpu, B):
+    """B rows of 151936 logits (a row splits over up to 16 workgroups, fewer as B grows):
+    per row the maximum repeated at random places (the first must win wherever the
+    copies fall), a unique maximum, or a near tie; ids and margins against numpy's first
+    argmax and the sorted top two."""
+    torch = torch_gpu
+    V = 151936
+    rng = np.random.default_rng(B)
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    for b in range(B):
+        kind = b % 3
+        if kind == 0:
+            at = rng.choice(V, size=int(rng.integers(2, 9)), replace=False)
+            x[b, at] = 7.5
+        elif kind == 1:
+            x[b, int(rng.integers(0, V))] = 8.0
+        else:
+            i, j = rng.choice(V, size=2, replace=False)
+            x[b, i], x[b, j] = 6.0, 6.0 - 2.0 ** -18
+    dx = torch.from_numpy(x).cuda()
+    ids = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    mg = torch.full((B,), -7.0, dtype=torch.float64, device="cuda")
+    ctx.greedy(dx, B, V, ids, mg)
+    torch.cuda.synchronize()
+    ids, mg = ids.cpu().numpy(), mg.cpu().numpy()
+    top = np.partition(x, V - 2, axis=1)[:, -2:].astype(np.float64)
+    assert np.array_equal(ids, np.argmax(x, axis=1))
+    assert np.array_equal(mg, top[:, 1] - top[:, 0])
+    assert np.array_equal(dx.cpu().numpy(), x)  # the logits are only read
+
+
 def test_refusals(ctx, torch_gpu):
     import tgo_amd
     x = torch_gpu.zeros(4, device="cuda")

@@ -67,6 +67,9 @@ def test_derived_ports_equal_the_packed_ports(torch_gpu, rows_pad):
     assert np.isfinite(la).all()
     assert np.array_equal(la, lb)
     assert np.array_equal(aa, ab)
+    # the idle member (extent 0): zero logits and no token
+    assert not la[1].any() and aa[1] == -1
+    assert la[0].any() and la[2].any() and aa[0] >= 0 and aa[2] >= 0
     # the KV pools the two steps wrote, every layer (padding rows write nothing)
     torch.cuda.synchronize()
     pools = [pool_copy(x) for x in (a, b)]

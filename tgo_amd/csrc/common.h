@@ -173,10 +173,14 @@ struct DeriveArgs {
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st);
 // keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1);
 // extents == null: every row is live. margin (nullable): the row's top-two
-// margin in float64 (TopTwoMargin).
-void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st, int keep_idle = 0, double* margin = nullptr);
-void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st);
+// margin in float64 (TopTwoMargin). zero_idle: the logits rows of members with
+// extent 0 are zeroed first. scratch: argmax_scratch_bytes(B, V) of device
+// memory for the per-chunk partials (a size that also serves any call with
+// fewer rows).
+size_t argmax_scratch_bytes(int B, int V);
+void launch_argmax(float* logits, int B, int V, const uint32_t* extents, int32_t* out,
+                   void* scratch, hipStream_t st, int keep_idle = 0, double* margin = nullptr,
+                   int zero_idle = 0);
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st);
 void launch_synth_absf16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,

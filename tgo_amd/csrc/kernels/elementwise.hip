@@ -7,7 +7,8 @@
 //   qk_rope_kv_kernel   q/k RMSNorm per head + interleaved RoPE + f16 narrowing +
 //                       ScatterRows into the paged pool, slot >= capacity dropped
 //                       (nn/attention.go:192-232, plan.go:182-192)
-//   argmax_kernel       greedy token, first strict maximum (sample/stages.go:196)
+//   argmax_*_kernel     greedy token, first strict maximum (sample/stages.go:196),
+//                       and the top-two margin
 //   synth_* kernels     seeded random-init weights, bit-identical to the CPU
 //                       restatement's generator
 #include "../common.h"
@@ -48,7 +49,9 @@ __global__ void embed_kernel(const uint32_t* ids, const void* table, const uint1
 // 1024 threads; wider rows loop): every load of a row is in flight at once.
 // With nsplit > 0 the residual add of a split-K projection is still pending:
 // x[src, :] += sum_s part[s][src, :] (summed in split order, as
-// gemm_reduce_kernel would) is done here first and written back to x.
+// gemm_reduce_kernel would) is done here first and written back to x. When
+// gathering (rows != null: the head's last rows, which two members may share)
+// the sum is used but x is left as it is.
 // acc += the N planes at p, p + plane, ... (element offset off), added in
 // plane order after all N loads are issued.
 template <int N>
@@ -107,14 +110,15 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t*
     float4_t v = *(const float4_t*)(x + src + i);
     if (nsplit > 0) {
       v += sum_planes(part, nsplit, plane, src + i);
-      *(float4_t*)(x + src + i) = v;
+      if (!rows) *(float4_t*)(x + src + i) = v;
     }
     ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
   }
   ss = block_sum(ss, red);
   const float sc = 1.0f / sqrtf(ss / (float)w + eps);
   for (int i = threadIdx.x * 4; i < w; i += step) {
-    const float4_t v = *(const float4_t*)(x + src + i);
+    float4_t v = *(const float4_t*)(x + src + i);
+    if (nsplit > 0 && rows) v += sum_planes(part, nsplit, plane, src + i);
     const float4_t gg = *(const float4_t*)(g + i);
     float4_t o;
 #pragma unroll
@@ -234,9 +238,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
 // First index of the strict maximum of each row (sample/stages.go:196-206).
 // Go's loop keeps best = x[0] and takes i only when x[i] > best: the first
 // index of the maximum, NaN never taken after index 0, and 0 when x[0] is NaN
-// or nothing exceeds it. One 1024-thread block per row; each thread scans its
-// 16-byte chunks in increasing index order, then the block reduces (larger
-// value, or equal value at a smaller index).
+// or nothing exceeds it.
 //
 // With margin != null the same pass gives TopTwoMargin
 // (internal/conformance/measure.go:91-110): the largest logit minus the
@@ -246,98 +248,140 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
 // reduction here keeps the top two of the non-NaN values and restates Go's
 // two seeded cases: x[0] NaN gives NaN, and x[1] NaN gives NaN unless a later
 // value exceeds x[0] (exactly when the argmax is not 0).
-// extents == null treats every row as live.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int V,
-                                                      const uint32_t* extents, int32_t* out,
-                                                      int keep_idle, double* margin) {
-  __shared__ float sv[16], s1[16], s2[16];
-  __shared__ int si[16];
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const float* row = logits + (size_t)b * V;
-  float best = -INFINITY, t1 = -INFINITY, t2 = -INFINITY;
-  int bi = 0x7fffffff;
-  auto take = [&](float v, int i) {
-    if (v > best) {
-      best = v;
-      bi = i;
+//
+// Two kernels. argmax_part_kernel: S workgroups per row, workgroup s scanning
+// the s-th contiguous chunk (whole float4s when V % 4 == 0), each thread its
+// elements in ascending order, leaving the chunk's (top1, top2, index of the
+// first top1) in part[b * S + s]. One workgroup per row left the C4 head's
+// 130 rows on half the CUs and VALU-bound (62 us for 79 MB). With zero_idle
+// the rows of members that contributed nothing (extents[b] == 0) are zeroed
+// instead of scanned. argmax_final_kernel: one thread per row merges its S
+// chunks and applies Go's x[0] / x[1] rules.
+struct Top2 {
+  float t1, t2;  // largest and second largest non-NaN values (-inf when none)
+  int i1;        // first index of t1 (0x7fffffff when none)
+  int pad;
+};
+
+// Folds (b1, b2, bi) into (t1, t2, i1): equal maxima keep the smaller index.
+__device__ __forceinline__ void top2_merge(float& t1, float& t2, int& i1, float b1, float b2,
+                                           int bi) {
+  if (b1 > t1 || (b1 == t1 && bi < i1)) i1 = bi;
+  const float lo = fminf(t1, b1), hi2 = fmaxf(t2, b2);  // t1, b1 are never NaN
+  t1 = fmaxf(t1, b1);
+  t2 = fmaxf(lo, hi2);
+}
+
+// Per element: the strict comparisons of Go's loops, NaN false in both.
+__device__ __forceinline__ void top2_take(float& t1, float& t2, int& i1, float v, int i) {
+  const bool c1 = v > t1, c2 = v > t2;
+  t2 = c1 ? t1 : (c2 ? v : t2);
+  t1 = c1 ? v : t1;
+  i1 = c1 ? i : i1;
+}
+
+constexpr int kArgmaxThreads = 256;
+
+// Chunks per row: about 512 workgroups in all, at most 16, each chunk at
+// least 4096 logits.
+static inline int argmax_chunks(int B, int V) {
+  int s = (512 + B - 1) / std::max(B, 1);
+  s = std::min(s, std::max(1, V / 4096));
+  return std::max(1, std::min(s, 16));
+}
+
+// B * argmax_chunks(B, V) <= B * ceil(512 / B) < 512 + B: enough for any
+// call with at most B rows, whatever V.
+size_t argmax_scratch_bytes(int B, int V) {
+  (void)V;
+  return (size_t)(512 + std::max(B, 0)) * sizeof(Top2);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(float* logits, int V, int S,
+                                                                     const uint32_t* extents,
+                                                                     int zero_idle, Top2* part) {
+  __shared__ float sv1[kArgmaxThreads / 64], sv2[kArgmaxThreads / 64];
+  __shared__ int si[kArgmaxThreads / 64];
+  const int b = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float* row = logits + (size_t)b * V;
+  const bool vec = (V & 3) == 0;  // rows 16-byte aligned: whole float4 chunks
+  const int units = vec ? V / 4 : V;
+  const int u0 = (int)((int64_t)units * s / S), u1 = (int)((int64_t)units * (s + 1) / S);
+  float t1 = -INFINITY, t2 = -INFINITY;
+  int i1 = 0x7fffffff;
+  if (zero_idle && extents[b] == 0) {
+    // an idle member's row: zeros (so the final pass gives 0 and margin 0)
+    for (int u = u0 + t; u < u1; u += kArgmaxThreads) {
+      if (vec) ((float4_t*)row)[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+      else row[u] = 0.f;
     }
-    if (v > t1) {
-      t2 = t1;
-      t1 = v;
-    } else if (v > t2) {
-      t2 = v;
-    }
-  };
-  const int V4 = V / 4;
-  const float4_t* row4 = (const float4_t*)row;  // rows are 16-byte aligned when V % 4 == 0
-  if ((V & 3) == 0) {
-    // Eight float4 loads in flight per thread (a loop of load-then-compare
-    // waited for each); the thread still visits its elements in ascending order.
-    int i4 = t;
-    for (; i4 + 7 * 1024 < V4; i4 += 8 * 1024) {
+    if (t == 0) part[(size_t)b * S + s] = Top2{0.f, u1 - u0 > 1 || vec ? 0.f : -INFINITY,
+                                               vec ? 4 * u0 : u0, 0};
+    return;
+  }
+  if (vec) {
+    // Eight float4 loads in flight per thread; its elements still in ascending order.
+    const float4_t* row4 = (const float4_t*)row;
+    int u = u0 + t;
+    for (; u + 7 * kArgmaxThreads < u1; u += 8 * kArgmaxThreads) {
       float4_t v[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = row4[i4 + u * 1024];
+      for (int k = 0; k < 8; k++) v[k] = row4[u + k * kArgmaxThreads];
 #pragma unroll
-      for (int u = 0; u < 8; u++)
+      for (int k = 0; k < 8; k++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) take(v[u][j], 4 * (i4 + u * 1024) + j);
+        for (int j = 0; j < 4; j++) top2_take(t1, t2, i1, v[k][j], 4 * (u + k * kArgmaxThreads) + j);
     }
-    for (; i4 < V4; i4 += 1024) {
-      const float4_t v = row4[i4];
+    for (; u < u1; u += kArgmaxThreads) {
+      const float4_t v = row4[u];
 #pragma unroll
-      for (int j = 0; j < 4; j++) take(v[j], 4 * i4 + j);
+      for (int j = 0; j < 4; j++) top2_take(t1, t2, i1, v[j], 4 * u + j);
     }
   } else {
-    for (int i = t; i < V; i += 1024) take(row[i], i);
+    for (int u = u0 + t; u < u1; u += kArgmaxThreads) top2_take(t1, t2, i1, row[u], u);
   }
-  // merge two (top1, top2) pairs: top1 = max, top2 = max(min(top1s), max(top2s))
-  auto merge = [&](float v2, int i2, float a1, float a2) {
-    if (v2 > best || (v2 == best && i2 < bi)) {
-      best = v2;
-      bi = i2;
-    }
-    const float lo = fminf(t1, a1), hi2 = fmaxf(t2, a2);
-    t1 = fmaxf(t1, a1);
-    t2 = fmaxf(lo, hi2);
-  };
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float v2 = __shfl_xor(best, o, 64);
-    const int i2 = __shfl_xor(bi, o, 64);
-    const float a1 = __shfl_xor(t1, o, 64), a2 = __shfl_xor(t2, o, 64);
-    merge(v2, i2, a1, a2);
+    const float b1 = __shfl_xor(t1, o, 64), b2 = __shfl_xor(t2, o, 64);
+    const int bi = __shfl_xor(i1, o, 64);
+    top2_merge(t1, t2, i1, b1, b2, bi);
   }
   if (lane == 0) {
-    sv[wave] = best;
-    si[wave] = bi;
-    s1[wave] = t1;
-    s2[wave] = t2;
+    sv1[wave] = t1;
+    sv2[wave] = t2;
+    si[wave] = i1;
   }
   __syncthreads();
   if (t == 0) {
-    for (int w = 1; w < 16; w++) merge(sv[w], si[w], s1[w], s2[w]);
-    // x[0] itself, and NaN at x[0], are Go's starting point
-    const float x0 = row[0];
-    int r = bi;
-    if (x0 != x0 || bi == 0x7fffffff || !(best > x0)) r = 0;
-    const bool live = !extents || extents[b] != 0;
-    if (live) out[b] = r;
-    else if (!keep_idle) out[b] = -1;
-    if (margin) {
-      const float x1 = row[1];
-      double mg = (double)t1 - (double)t2;
-      if (x0 != x0 || (x1 != x1 && r == 0)) mg = __builtin_nan("");
-      margin[b] = mg;
-    }
+    for (int w = 1; w < kArgmaxThreads / 64; w++) top2_merge(t1, t2, i1, sv1[w], sv2[w], si[w]);
+    part[(size_t)b * S + s] = Top2{t1, t2, i1, 0};
   }
 }
 
-// Zeroes the logits rows of members that contributed nothing.
-__global__ void zero_idle_rows_kernel(float* logits, int V, const uint32_t* extents) {
-  const int b = blockIdx.x;
-  if (extents[b] != 0) return;
-  for (int i = threadIdx.x; i < V; i += blockDim.x) logits[(size_t)b * V + i] = 0.f;
+// extents == null treats every row as live.
+__global__ void argmax_final_kernel(const float* logits, int B, int V, int S,
+                                    const uint32_t* extents, const Top2* part, int32_t* out,
+                                    int keep_idle, double* margin) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const Top2* p = part + (size_t)b * S;
+  float t1 = p[0].t1, t2 = p[0].t2;
+  int i1 = p[0].i1;
+  for (int s = 1; s < S; s++) top2_merge(t1, t2, i1, p[s].t1, p[s].t2, p[s].i1);
+  // x[0] itself, and NaN at x[0], are Go's starting point
+  const float* row = logits + (size_t)b * V;
+  const float x0 = row[0];
+  int r = i1;
+  if (x0 != x0 || i1 == 0x7fffffff || !(t1 > x0)) r = 0;
+  const bool live = !extents || extents[b] != 0;
+  if (live) out[b] = r;
+  else if (!keep_idle) out[b] = -1;
+  if (margin) {
+    const float x1 = row[1];
+    double mg = (double)t1 - (double)t2;
+    if (x0 != x0 || (x1 != x1 && r == 0)) mg = __builtin_nan("");
+    margin[b] = mg;
+  }
 }
 
 // ---- seeded synthesis (the CPU restatement's generator, restated) ---------
@@ -466,13 +510,14 @@ void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   const int gy = T >= 512 ? 1 : groups;
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T, gy), dim3(256), 0, st, a);
 }
-void launch_argmax(const float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   hipStream_t st, int keep_idle, double* margin) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(1024), 0, st, logits, V, extents, out, keep_idle,
-                     margin);
-}
-void launch_zero_idle(float* logits, int B, int V, const uint32_t* extents, hipStream_t st) {
-  hipLaunchKernelGGL(zero_idle_rows_kernel, dim3(B), dim3(256), 0, st, logits, V, extents);
+void launch_argmax(float* logits, int B, int V, const uint32_t* extents, int32_t* out,
+                   void* scratch, hipStream_t st, int keep_idle, double* margin, int zero_idle) {
+  if (B <= 0) return;
+  const int S = argmax_chunks(B, V);
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(B, S), dim3(kArgmaxThreads), 0, st, logits, V, S,
+                     extents, zero_idle, (Top2*)scratch);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3((B + 63) / 64), dim3(64), 0, st, logits, B, V, S,
+                     extents, (const Top2*)scratch, out, keep_idle, margin);
 }
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st) {

@@ -140,6 +140,7 @@ struct tgohip_ctx {
   int cascade = 0;    // minimum sequences sharing a prefix for prefix-shared attention (0: off)
   // activations and workspaces
   DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, margin, meta, gemm_ws, part_o, part_ml;
+  DevBuf amax_part;  // per-chunk partials of the greedy selection
   DevBuf rows;  // [2][rows]: positions and slots derived on the device
   int rows_cap = 0, batch_cap = 0;
   // pinned staging for per-step metadata
@@ -455,6 +456,7 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
     if ((rc = c->logits.ensure((size_t)B * m.vocab * 4))) return rc;
     if ((rc = c->argmax.ensure((size_t)B * 4))) return rc;
     if ((rc = c->margin.ensure((size_t)B * 8))) return rc;
+    if ((rc = c->amax_part.ensure(argmax_scratch_bytes(B, m.vocab)))) return rc;
     c->batch_cap = B;
   }
   // split-K workspace: the largest any projection of this step may ask for
@@ -532,7 +534,7 @@ void tgohip_close(tgohip_ctx* c) {
   for (void* p : c->allocs) (void)hipFree(p);
   c->allocs.clear();
   for (DevBuf* b : {&c->h, &c->xn, &c->qkv, &c->q, &c->attn, &c->act, &c->lastn, &c->logits,
-                    &c->argmax, &c->margin, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml,
+                    &c->argmax, &c->margin, &c->amax_part, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml,
                     &c->rows})
     b->release();
   if (c->kc) (void)hipFree(c->kc);
@@ -999,22 +1001,21 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                            f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_GATEUP, l, 1))) return rc;
-    // the last layer's residual add completes here (the head reads only Last rows)
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st,
-                           l + 1 < m.layers ? &pend : nullptr)))
+    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 1))) return rc;
-    if (l + 1 == m.layers) pend = 0;
   }
-  launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p, actf16, st);
+  // The last layer's split residual add is summed for the Last rows only (the
+  // head reads nothing else); h keeps the rows without it.
+  launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p,
+                 actf16, st, ws, pend, plane);
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 0))) return rc;
   if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 1))) return rc;
-  launch_zero_idle((float*)c->logits.p, B, m.vocab, d_ext, st);
-  launch_argmax((const float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, st, o.keep_idle,
-                (double*)c->margin.p);
+  launch_argmax((float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, c->amax_part.p, st,
+                o.keep_idle, (double*)c->margin.p, 1);
   TGOHIP_HIP(hipEventRecord(o.ev_end, st));
   TGOHIP_HIP(hipGetLastError());
   return 0;
@@ -1095,7 +1096,11 @@ int tgohip_greedy(tgohip_ctx* c, const float* logits, int B, int V, int32_t* ids
                                    " logits; the top-two margin is over at least two");
   if (B == 0) return 0;
   if (!logits || !ids) return fail(TGOHIP_EINVAL, "greedy: logits and ids are device buffers");
-  launch_argmax(logits, B, V, nullptr, ids, c->stream, 0, margins);
+  int rc;
+  if ((rc = c->amax_part.ensure(argmax_scratch_bytes(B, V)))) return rc;
+  // the logits are only read (no idle rows to zero)
+  launch_argmax(const_cast<float*>(logits), B, V, nullptr, ids, c->amax_part.p, c->stream, 0,
+                margins, 0);
   TGOHIP_HIP(hipGetLastError());
   return 0;
 }
