@@ -1207,11 +1207,25 @@ static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st
 // half the chip's slots (2 per CU); otherwise as many splits as fit in one
 // round of slots, keeping >= 8 k-steps per split.
 // slots: workgroups the chip holds at once.
+// TGOHIP_GEMM_MAX_SPLITS (1-8, default 8): the most split-K slices. At the
+// C4 decode step (128 rows) a cap of 4 (fewer partial planes for QKV and O)
+// or a rule keeping the planes' bytes below the weights' ran within the
+// run-to-run spread of 8 over 4 alternating pairs of 300 steps (10.64-10.91
+// against 10.62-10.65 ms); a cap of 2 was 5% slower.
+static int pipe_max_splits() {
+  static const int v = [] {
+    const char* e = getenv("TGOHIP_GEMM_MAX_SPLITS");
+    const int n = e ? atoi(e) : 8;
+    return n >= 1 && n <= 8 ? n : 8;
+  }();
+  return v;
+}
+
 static int choose_pipe_splits(int tiles, int KS, int slots) {
   if (tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
   int s = slots / tiles;              // one round of workgroups
   while (s > 1 && KS / s < 8) s--;
-  return std::max(1, std::min(s, 8));
+  return std::max(1, std::min(s, pipe_max_splits()));
 }
 
 // Row-tile height and split-K of the pipelined kernel. Up to 384 rows, 64-row
