@@ -88,6 +88,16 @@ __device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const
 // uint4): copies through it are plain loads and stores, so the arrays of
 // chunks a wave keeps in flight stay in registers.
 typedef uint32_t kv16_t __attribute__((ext_vector_type(4)));
+// A decode item's K/V rows are read once per launch: non-temporal loads (the
+// nt bit) stream them. A plain 4 GiB read on this part runs at 6.2 TB/s with
+// ordinary 16-byte loads and 7.0 TB/s with nt ones; the C4 step's attention
+// launch went from 4.4-4.5 to 5.0-5.2 TB/s (decode-only step 5.1-5.3 to
+// 5.9-6.0). Prefill items keep ordinary loads: the items of one (sequence,
+// kv head) re-read the same K/V through their XCD's L2, and nt loads there
+// cost the C4 step 2.5%.
+__device__ __forceinline__ kv16_t kv_load_nt(const half_t* p) {
+  return __builtin_nontemporal_load((const kv16_t*)p);
+}
 
 constexpr int kMaxItemPages = 1024;        // page indices an item stages in LDS
 constexpr int kAttnVBytes = 20480;         // one V tile in LDS (64 padded rows)
@@ -207,17 +217,17 @@ __device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx
       const int iv = min((pv >> 4) - c.pg0, kMaxItemPages - 1);
       const uint32_t krow = c.pg[ik] * 16u + (uint32_t)(pk & 15);
       const uint32_t vrow = c.pg[iv] * 16u + (uint32_t)(pv & 15);
-      kr[i] = *(const kv16_t*)(a.k + krow * c.rstride + c.lane_off);
-      vr[i] = *(const kv16_t*)(a.v + vrow * c.rstride + c.lane_off);
+      kr[i] = kv_load_nt(a.k + krow * c.rstride + c.lane_off);
+      vr[i] = kv_load_nt(a.v + vrow * c.rstride + c.lane_off);
     }
     return;
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pk = p0 + prow + 4 * i, pv = p0 + 4 * prow + i;
-    kr[i] = pk < hi ? *(const kv16_t*)(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+    kr[i] = pk < hi ? kv_load_nt(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
                     : kv16_t{0u, 0u, 0u, 0u};
-    vr[i] = pv < hi ? *(const kv16_t*)(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+    vr[i] = pv < hi ? kv_load_nt(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
                     : kv16_t{0u, 0u, 0u, 0u};
   }
 }
