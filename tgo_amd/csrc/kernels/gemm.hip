@@ -117,29 +117,49 @@ template <> struct BRaw<TGOHIP_FORM_I8> { uint4 p[2]; uint4 s[4]; };
 template <> struct BRaw<TGOHIP_FORM_I4_TGO> { uint4 p; uint4 s[4]; uint4 z[4]; };
 template <> struct BRaw<TGOHIP_FORM_I4_SYM> { uint4 p; uint32_t s; };
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// A 16-byte weight load; NT: non-temporal (the nt bit), for a launch that
+// reads each weight once. The small-M kernel's int4 gate/up at one row went
+// from 15.6 to 13.5 us with it, the LM head from 70.7 to 64.8; the pipelined
+// kernel's row tiles share weights through L2, and nt loads made its 64- and
+// 128-row down 12-18% slower.
+template <bool NT>
+__device__ __forceinline__ uint4 ldw16(const void* p) {
+  if constexpr (NT) {
+    const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *(const uint4*)p;
+  }
+}
+
+template <bool NT = false>
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
                                           BRaw<TGOHIP_FORM_F16>& r) {
   const size_t slot = ((size_t)nb * (g.K / 64) + ks) * 64 + lane;
   const uint4* pp = (const uint4*)((const char*)g.wp + slot * 64);
 #pragma unroll
-  for (int i = 0; i < 4; i++) r.p[i] = pp[i];
+  for (int i = 0; i < 4; i++) r.p[i] = ldw16<NT>(pp + i);
 }
+template <bool NT = false>
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
                                           BRaw<TGOHIP_FORM_I8>& r) {
   const int KS = g.K / 64;
   const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
   const uint4* pp = (const uint4*)((const char*)g.wp + slot * 32);
-  r.p[0] = pp[0];
-  r.p[1] = pp[1];
+  r.p[0] = ldw16<NT>(pp);
+  r.p[1] = ldw16<NT>(pp + 1);
   const int h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; j++) r.s[j] = *(const uint4*)(g.ws + ((((size_t)nb * KS + ks) * 4 + j) * 2 + h) * 8);
 }
+template <bool NT = false>
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
                                           BRaw<TGOHIP_FORM_I4_TGO>& r) {
   const int KS = g.K / 64;
   const size_t slot = ((size_t)nb * KS + ks) * 64 + lane;
-  r.p = *(const uint4*)((const char*)g.wp + slot * 16);
+  r.p = ldw16<NT>((const char*)g.wp + slot * 16);
   const int h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -148,12 +168,13 @@ __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int
     r.z[j] = *(const uint4*)(g.wz + o);
   }
 }
+template <bool NT = false>
 __device__ __forceinline__ void load_braw(const GemmArgs& g, int nb, int ks, int lane,
                                           BRaw<TGOHIP_FORM_I4_SYM>& r) {
   // (nb, ks) is uniform across the wave: a scalar base plus a 32-bit lane
   // offset, so the loads need no 64-bit vector address arithmetic.
   const size_t blk = (size_t)nb * (g.K / 64) + ks;
-  r.p = *(const uint4*)((const char*)g.wp + blk * 1024 + (uint32_t)lane * 16u);
+  r.p = ldw16<NT>((const char*)g.wp + blk * 1024 + (uint32_t)lane * 16u);
   r.s = *(const uint32_t*)((const char*)g.ws + blk * 128 + (uint32_t)(lane & 31) * 4u);
 }
 
@@ -162,7 +183,6 @@ __device__ __forceinline__ uint32_t word_of(const uint4& p, int j) {
 }
 
 union U16B { uint4 u; half8_t h; };
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_F16>& r, int j) {
   U16B c;
@@ -991,7 +1011,7 @@ __global__ __launch_bounds__(64 * W) void gemm_gemv_kernel(GemmArgs g) {
   };
   auto load = [&](int d, int ks) {
 #pragma unroll
-    for (int b = 0; b < CB; b++) load_braw(g, nbl[b], ks, lane, bq[d][b]);
+    for (int b = 0; b < CB; b++) load_braw<true>(g, nbl[b], ks, lane, bq[d][b]);
     if constexpr (!STAGED) load_a(aq[d], ks);
   };
 #pragma unroll
@@ -1246,10 +1266,18 @@ static int choose_pipe_splits(int tiles, int KS, int slots) {
 static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, int& tiles_n,
                        int& tiles, int& splits, int epi = EPI_F32) {
   mw = M <= 384 ? 64 : 128;
-  const int nb = w.N / 32;
-  nw = (mw == 128 && ((nb + 15) / 16) % 8 == 0) ? 8 : 4;
+  const int nb = w.N / 32, rows = (M + mw - 1) / mw;
+  nw = 4;
+  if (mw == 128) {
+    // 8 waves wide when the wide tiles deal evenly over the XCDs: over all 8
+    // unsplit, or over the 8/s XCDs of a split when split-K slices them.
+    const int tn8 = (nb + 15) / 16;
+    const int s8 = choose_pipe_splits(tn8 * rows, w.K / 64, ncu);
+    const int g8 = (s8 == 2 || s8 == 4 || s8 == 8) ? 8 / s8 : 8;
+    if (tn8 % g8 == 0) nw = 8;
+  }
   tiles_n = (nb + 2 * nw - 1) / (2 * nw);
-  tiles = tiles_n * ((M + mw - 1) / mw);
+  tiles = tiles_n * rows;
   splits = choose_pipe_splits(tiles, w.K / 64, ncu * (8 / nw));
   if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) && tiles >= ncu / 2) splits = 1;
 }
