@@ -123,7 +123,7 @@ def achievable_peaks(ctx):
         "read_gbps": round(read_gbps, 1),
         "mfma_f16_tflops": round(mfma_tflops, 1),
         "how": "tgohip_probe_peaks before the timed region: a grid-stride read of 2 GiB "
-               "(16-byte loads) and independent v_mfma_f32_32x32x16_f16 chains on every CU; "
+               "(16-byte non-temporal loads) and independent v_mfma_f32_32x32x16_f16 chains on every CU; "
                "medians of 5",
     }
 

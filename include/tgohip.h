@@ -382,7 +382,7 @@ int tgohip_profile_read_kernel(tgohip_ctx* ctx, int kind, double* ms, double* by
                                double* flops, int64_t* launches);
 /* What this box reaches (measurement helper, no counterpart in the reference;
  * the benchmark reports it beside the published peaks): a streaming read of
- * read_bytes (16-byte loads, grid-stride; a buffer the call allocates, fills
+ * read_bytes (16-byte non-temporal loads, grid-stride; a buffer the call allocates, fills
  * and frees) and a dense f16 MFMA loop (independent v_mfma_f32_32x32x16_f16
  * chains, four waves per workgroup, four workgroups per CU); medians of reps
  * timed launches on the context's stream. */

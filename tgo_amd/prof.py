@@ -135,7 +135,8 @@ XCDS = 8      # GRBM_GUI_ACTIVE is reported summed over the XCDs
 def label_projections(names):
     """The projection each GEMM dispatch computes, from the step's launch order: per layer
     rmsnorm, QKV, qk_rope_kv, attention (+ combine), O, rmsnorm, gate/up, down; after the
-    last layer a gathered rmsnorm and the LM head, followed by zero_idle_rows_kernel."""
+    last layer a gathered rmsnorm and the LM head, followed by the greedy selection
+    (argmax_part_kernel; zero_idle_rows_kernel in traces of earlier builds)."""
     labels = [None] * len(names)
     prev_gemm = None
     for i, n in enumerate(names):
@@ -144,7 +145,7 @@ def label_projections(names):
         before = next((names[j] for j in range(i - 1, -1, -1)
                        if "gemm_reduce" not in names[j]), "")
         after = names[i + 1] if i + 1 < len(names) else ""
-        if "zero_idle" in after:
+        if "zero_idle" in after or "argmax" in after:
             lab = "lm_head"
         elif "attn_" in before:
             lab = "o"
