@@ -5,8 +5,8 @@ against tgo's CPU path restated (orc_model_step) on identical inputs
 * C4: Qwen3-8B widths (hidden 4096, 32/8 heads, MLP 12288, vocab 151936), int4 (the
   symmetric g32-K pack), page 16, driven by bench.py's workload through the library
   Scheduler: 128 decoding sequences with lognormal(1024, 1.0) contexts clipped to
-  [16, 8192] plus 2 prefill chunks of 512 -- 130 members, 1152 rows. Both activation
-  precisions.
+  [16, 8192] plus 2 prefill chunks of 512 -- 130 members, 1152 rows; and the
+  decode-dominated step, the 128 decoders alone (128 rows). Both activation precisions.
 * C5: Qwen3-32B widths (hidden 5120, 64/8 heads, MLP 25600), int8, 256 decoding
   sequences on one 2048-token shared prefix (suffixes U[32, 1024]) plus one 1024-token
   chunk, prefix-shared attention on and off.
@@ -112,6 +112,43 @@ def test_c4_step_matches_the_cpu_path(torch_gpu):
             n, nt = compare(logits, ids, want, st["extents"], "C4 precision %d" % precision)
             decisions, near = decisions + n, near + nt
         assert decisions == 2 * 130
+        assert len(near) <= 0.02 * decisions, near
+    finally:
+        if cpu:
+            cpu.close()
+        ctx.close()
+
+
+@pytest.mark.timeout(900)
+def test_c4_decode_step_matches_the_cpu_path(torch_gpu):
+    """The decode-dominated step bench.py reports beside the headline: C4's 128 decoders
+    alone (the two requests mid-prefill finished), 128 rows -- 64-row GEMM tiles, the SwiGLU
+    gate/up with two k groups per workgroup, 8-way split-K for QKV, O and down, decode-only
+    attention -- both precisions."""
+    cfg, form, pool = bench.C4, tgo_amd.FORM_I4_SYM, bench.POOL
+    ctx = open_ctx(cfg, form, pool, bench.SEED)
+    cpu = None
+    try:
+        wl = bench.Workload(tgo_amd, ctx, bench.SEED)
+        ctx.kv_synth(bench.SEED, 1.0, min(pool, wl.used_positions + 64 * bench.CHUNK))
+        wl.decode_only()
+        cpu = cpu_model(cfg, form, pool, bench.SEED)
+        copy_pool(ctx, cpu, LAYERS, cfg["kv_heads"], pool)
+        produced, prefill, decodes, _ = wl.sched.step()
+        assert (prefill, decodes) == (0, bench.DECODERS)
+        st, pages, maxp = wl.sched.last_step()
+        assert len(st["ids"]) == bench.DECODERS
+        want = cpu.step(st, pages, maxp, layers=LAYERS)
+        near, decisions = [], 0
+        for precision in (0, 1):
+            ctx.set_precision(precision)
+            logits, ids, _ = ctx.step(st, pages, maxp)
+            if precision == 0:
+                for slot, tok, done in produced:
+                    assert tok == int(ids[slot]), (slot, tok, int(ids[slot]))
+            n, nt = compare(logits, ids, want, st["extents"], "C4 decode precision %d" % precision)
+            decisions, near = decisions + n, near + nt
+        assert decisions == 2 * bench.DECODERS
         assert len(near) <= 0.02 * decisions, near
     finally:
         if cpu:
