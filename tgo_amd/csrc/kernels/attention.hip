@@ -300,10 +300,15 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Tiles of loads a decode-style item keeps in flight (its registers are free:
-// the prefill path sets the kernel's register budget).
+// Blocks of loads a decode-style item keeps in flight beside the one it
+// computes on. With the non-temporal K/V loads one is enough (a CU's 8 waves
+// then hold 64 KiB in flight, 16 MiB over the chip): against 3 (the depth
+// with ordinary loads) the decode-only step went from 10.26-10.28 to
+// 10.02-10.05 ms with 2 and to 10.00-10.05 with 1 (10.21-10.24 with 2 on
+// that box), and the mixed step was the same with 1 and 2 and 1% slower
+// with 3.
 #ifndef TGOHIP_DECODE_DEPTH
-#define TGOHIP_DECODE_DEPTH 3
+#define TGOHIP_DECODE_DEPTH 1
 #endif
 constexpr int kDecodeDepth = TGOHIP_DECODE_DEPTH;
 
