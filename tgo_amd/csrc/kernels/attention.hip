@@ -1048,9 +1048,15 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
     else if (q_f16) hipLaunchKernelGGL((attn_kernel<0, true>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((attn_kernel<0, false>), grid, dim3(256), 0, stream, a);
   }
-  if (!plan.combines.empty())
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)plan.combines.size(), kAttnRowsP / 16),
-                       dim3(256), 0, stream, a);
+  if (!plan.combines.empty()) {
+    // 16 rows per block: as many row blocks as the largest item needs (a
+    // decode-only step's items have G rows: one block each, not eight)
+    int rows = 1;
+    for (const AttnCombine& x : plan.combines) rows = std::max(rows, x.ntok * H / Hkv);
+    const unsigned ry = (unsigned)std::min((rows + 15) / 16, kAttnRowsP / 16);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)plan.combines.size(), ry), dim3(256), 0,
+                       stream, a);
+  }
   if (plan.claimed < T) {
     const size_t start = (size_t)plan.claimed * H * kHeadDim;
     const size_t count = (size_t)(T - plan.claimed) * H * kHeadDim;
