@@ -216,6 +216,35 @@ def test_small_batch_step_on_the_small_m_kernel(torch_gpu, form):
         cpu.close()
 
 
+@pytest.mark.parametrize("form", [0, 1, 2, 3])
+def test_wide_chunk_step_with_two_k_groups(torch_gpu, form):
+    """Qwen3-8B-wide projections at 100 rows (a 96-token chunk beside four decodes): the
+    SwiGLU gate/up (N = 24576) runs 64-row tiles with two k groups per workgroup (its 192
+    tiles leave at most one workgroup per CU), QKV, O and down split-K; every form,
+    against the CPU path."""
+    cfg = dict(WIDE, positions=1024)
+    ctx, cpu = make_pair(torch_gpu, cfg, form, 61 + form, 0)
+    try:
+        engines = [Engine(b, cfg["vocab"], cfg["heads"], cfg["kv_heads"], cfg["positions"],
+                          cfg["block"], 5) for b in (gpu_backend(ctx), cpu_backend(cpu))]
+        rng = np.random.default_rng(70 + form)
+        prompts = [[int(t) for t in rng.integers(0, cfg["vocab"], n)] for n in (5, 9, 3, 7)]
+        for e in engines:
+            for i, p in enumerate(prompts):
+                e.admit(i, p, 4)
+        outs = [e.step([(i, p) for i, p in enumerate(prompts)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1, 2, 3], "prefill")
+        chunk = [int(t) for t in rng.integers(0, cfg["vocab"], 96)]
+        for e in engines:
+            e.admit(4, chunk, 4)
+        nxt = [argmax_first(outs[1][i]) for i in range(4)]
+        outs = [e.step([(i, [nxt[i]]) for i in range(4)] + [(4, chunk)]) for e in engines]
+        check_logits(outs[0], outs[1], [0, 1, 2, 3, 4], "decodes + chunk of 96")
+    finally:
+        ctx.close()
+        cpu.close()
+
+
 @pytest.mark.parametrize("form", [3, 0])
 def test_long_chunk_step_matches_the_cpu_path(torch_gpu, form):
     """A 150-token chunk beside two decodes: the projections run at M >= 96 (the
