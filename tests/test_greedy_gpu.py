@@ -1,5 +1,5 @@
-"""The device greedy kernel (tgohip_greedy: argmax_kernel) on crafted rows, against the
-Go loops it restates, run on the host (oracle/host.py):
+"""The device greedy selection (tgohip_greedy: argmax_part_kernel + argmax_final_kernel)
+on crafted rows, against the Go loops it restates, run on the host (oracle/host.py):
 
   * argmax (sample/stages.go:196-206): best = x[0], then i taken only when x[i] > best --
     the first index of the maximum, a NaN never taken after index 0, 0 when x[0] is NaN;
@@ -9,7 +9,7 @@ Go loops it restates, run on the host (oracle/host.py):
 Both bit-exact (ids equal; margins equal as float64, NaN where Go gives NaN). The rows
 cover the reference's known answers (tests/golden), ties, NaN at index 0, 1 and later,
 +-inf, all-equal rows, V not a multiple of 4, V = 2 and the C4 vocabulary with the
-maximum in the first, a middle and the last 16-byte chunk of a thread's stride."""
+maximum at chunk and stride edges, and batches whose rows split over 1 to 16 workgroups."""
 import json
 import math
 import os
@@ -78,9 +78,9 @@ def test_crafted_rows(ctx, torch_gpu, V):
 
 
 def test_vocabulary_rows_with_the_maximum_everywhere(ctx, torch_gpu):
-    """V = 151936: one thread scans 16-byte chunks 4096 floats apart; the maximum placed
-    in each part of that stride, ties across threads and waves resolved to the lowest
-    index."""
+    """V = 151936 over 16 workgroups per row (a thread's 16-byte chunks 1024 floats apart
+    in its workgroup's chunk of the row): the maximum placed at both ends and inside,
+    ties across threads, waves and workgroups resolved to the lowest index."""
     V = 151936
     rng = np.random.default_rng(1)
     rows = []
