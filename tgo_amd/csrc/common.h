@@ -43,8 +43,12 @@ struct AttnItem {
   int32_t mode;  // 0: rows <= 16, the four waves split the positions; 1: waves split rows;
                  // 2: an empty slot of the launch order; 3: a shared prefix: rows are
                  // the decode tokens of sequences seqlist[tok0 .. tok0+ntok) (G rows
-                 // each), pages those of `seq`, every position visible
+                 // each), pages those of `seq`, every position visible. Mode 0 with
+                 // kAttnSharedPages set: the item's positions include pages another
+                 // sequence also reads (ordinary loads, not non-temporal ones).
 };
+constexpr int kAttnModeMask = 15;
+constexpr int kAttnSharedPages = 16;
 // One combine item: merges the partial results of a (sequence, kv head,
 // tokens): first xparts parts of a shared prefix (the sequence's rows sit at
 // row xrow of those parts), then nparts parts of its own positions.

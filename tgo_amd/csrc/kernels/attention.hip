@@ -98,6 +98,15 @@ typedef uint32_t kv16_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ kv16_t kv_load_nt(const half_t* p) {
   return __builtin_nontemporal_load((const kv16_t*)p);
 }
+// A decode item over pages other sequences also read (a shared prefix
+// without the cascade) keeps ordinary loads, so the caches serve the other
+// sequences' reads of the same pages: with non-temporal loads the config-5
+// shape without the cascade took 0.50 ms per launch instead of 0.44.
+template <bool SHARED>
+__device__ __forceinline__ kv16_t kv_load_dec(const half_t* p) {
+  if constexpr (SHARED) return *(const kv16_t*)p;
+  else return kv_load_nt(p);
+}
 
 constexpr int kMaxItemPages = 1024;        // page indices an item stages in LDS
 constexpr int kAttnVBytes = 20480;         // one V tile in LDS (64 padded rows)
@@ -200,7 +209,7 @@ __device__ __forceinline__ void attn_store_tile(const AttnCtx& c, half_t* Ks, ha
 // A decode wave's own 16 positions p0 + [0,16) of a tile: lane (dch, prow) =
 // (lane % 16, lane / 16) loads K positions p0 + prow + 4i and V positions
 // p0 + 4prow + i, dims 8*dch + [0,8). Positions at or past hi load zeros.
-template <int BLK>
+template <int BLK, bool SHARED>
 __device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx& c, int p0, int hi,
                                                 int prow, kv16_t (&kr)[4], kv16_t (&vr)[4]) {
   if (BLK == 16) {
@@ -217,17 +226,17 @@ __device__ __forceinline__ void attn_load_block(const AttnArgs& a, const AttnCtx
       const int iv = min((pv >> 4) - c.pg0, kMaxItemPages - 1);
       const uint32_t krow = c.pg[ik] * 16u + (uint32_t)(pk & 15);
       const uint32_t vrow = c.pg[iv] * 16u + (uint32_t)(pv & 15);
-      kr[i] = kv_load_nt(a.k + krow * c.rstride + c.lane_off);
-      vr[i] = kv_load_nt(a.v + vrow * c.rstride + c.lane_off);
+      kr[i] = kv_load_dec<SHARED>(a.k + krow * c.rstride + c.lane_off);
+      vr[i] = kv_load_dec<SHARED>(a.v + vrow * c.rstride + c.lane_off);
     }
     return;
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int pk = p0 + prow + 4 * i, pv = p0 + 4 * prow + i;
-    kr[i] = pk < hi ? kv_load_nt(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
+    kr[i] = pk < hi ? kv_load_dec<SHARED>(a.k + attn_row_of(c, pk) * c.rstride + c.lane_off)
                     : kv16_t{0u, 0u, 0u, 0u};
-    vr[i] = pv < hi ? kv_load_nt(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
+    vr[i] = pv < hi ? kv_load_dec<SHARED>(a.v + attn_row_of(c, pv) * c.rstride + c.lane_off)
                     : kv16_t{0u, 0u, 0u, 0u};
   }
 }
@@ -325,7 +334,9 @@ constexpr float kLazyMax = 8.f;
 // The four waves take the four 16-position blocks of each 64-position tile and
 // merge their softmax states at the end. kDecodeDepth tiles of loads are in
 // flight.
-template <int BLK, bool QF16>
+// SHARED: the item's positions include pages other sequences read too
+// (ordinary loads); otherwise non-temporal ones.
+template <int BLK, bool QF16, bool SHARED>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& it, const AttnCtx& c,
                                             char* smem) {
   const float qs = attn_qscale<QF16>(a);
@@ -368,7 +379,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
   static_for<D>([&](auto uc) {
     constexpr int u = decltype(uc)::value;
     if (kAlways || it.kv_lo + u * kAttnTile < it.kv_hi)
-      attn_load_block<BLK>(a, c, it.kv_lo + u * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
+      attn_load_block<BLK, SHARED>(a, c, it.kv_lo + u * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
   });
   for (int tt = it.kv_lo; tt < it.kv_hi; tt += D * kAttnTile) {
     static_for<D>([&](auto uc) {
@@ -376,7 +387,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
       const int t0 = tt + u * kAttnTile;
       if (t0 < it.kv_hi) attn_store_block(Kw, Vw, li, lg, kr[u], vr[u]);
       if (kAlways || t0 + D * kAttnTile < it.kv_hi)
-        attn_load_block<BLK>(a, c, t0 + D * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
+        attn_load_block<BLK, SHARED>(a, c, t0 + D * kAttnTile + wofs, it.kv_hi, lg, kr[u], vr[u]);
       if (t0 < it.kv_hi) {
 
         // Scores of this wave's 16-position block.
@@ -651,11 +662,11 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
 // BLK is the page size when it is 16 (the fast path: a 64-position tile is
 // four whole pages), or 0 for any other page size.
 // DEC: a launch of decode-style items only (a decode-only step). Without the
-// prefill path the kernel needs 124 VGPRs instead of 218, so four workgroups
+// prefill path the kernel fits 128 VGPRs instead of 218, so four workgroups
 // share a CU instead of two: the C4 decode-only step's attention launch
 // 0.1634-0.1638 -> 0.1622-0.1624 ms (three alternating pairs).
 template <int BLK, bool QF16, bool DEC = false>
-__global__ __launch_bounds__(256, DEC ? 3 : 2) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, DEC ? 4 : 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmem];
   const AttnItem it = a.items[blockIdx.x];
   if (it.mode == 2) return;  // an empty slot of the XCD-aware order
@@ -685,12 +696,14 @@ __global__ __launch_bounds__(256, DEC ? 3 : 2) void attn_kernel(AttnArgs a) {
   c.lane_off = (uint32_t)c.kvh * kHeadDim + c.dch * 8;
   __syncthreads();  // pg visible
   if constexpr (DEC) {
-    attn_decode<BLK, QF16>(a, it, c, smem);
-  } else if (it.mode == 0) {
+    if (it.mode & kAttnSharedPages) attn_decode<BLK, QF16, true>(a, it, c, smem);
+    else attn_decode<BLK, QF16, false>(a, it, c, smem);
+  } else if ((it.mode & kAttnModeMask) == 0) {
     // Decode waves are HBM streams: raised priority lets their loads and short
     // softmax steps issue ahead of a co-resident prefill item's MFMA work.
     __builtin_amdgcn_s_setprio(1);
-    attn_decode<BLK, QF16>(a, it, c, smem);
+    if (it.mode & kAttnSharedPages) attn_decode<BLK, QF16, true>(a, it, c, smem);
+    else attn_decode<BLK, QF16, false>(a, it, c, smem);
   } else {
     attn_prefill<BLK, QF16>(a, it, c, smem);
   }
@@ -881,6 +894,42 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       i = j;
     }
   }
+  // Leading pages a sequence shares with another (first page equal, then the
+  // run of equal pages with the first sequence of that page): decode items
+  // below that many positions use ordinary loads (kAttnSharedPages). The
+  // cascade's suffix items start past its prefix.
+  std::vector<int64_t> spos(B, 0);
+  {
+    std::vector<std::pair<uint32_t, int>> firsts;
+    for (int s = 0; s < B; s++)
+      if (extents[s] > 0 && lengths[s] > 0) firsts.push_back({pages[(size_t)s * max_pages], s});
+    std::stable_sort(firsts.begin(), firsts.end(),
+                     [](const std::pair<uint32_t, int>& x, const std::pair<uint32_t, int>& y) {
+                       return x.first < y.first;
+                     });
+    for (size_t i = 0; i < firsts.size();) {
+      size_t j = i + 1;
+      while (j < firsts.size() && firsts[j].first == firsts[i].first) j++;
+      if (j - i >= 2) {
+        const int lead = firsts[i].second;
+        const uint32_t* lrow = pages + (size_t)lead * max_pages;
+        const int64_t lp = ((int64_t)lengths[lead] + block - 1) / block;
+        int64_t lead_shared = 0;
+        for (size_t k = i + 1; k < j; k++) {
+          const int sq = firsts[k].second;
+          const uint32_t* row = pages + (size_t)sq * max_pages;
+          const int64_t need = std::min<int64_t>(((int64_t)lengths[sq] + block - 1) / block, lp);
+          int64_t cp = 0;
+          while (cp < need && row[cp] == lrow[cp]) cp++;
+          spos[sq] = cp * block;
+          lead_shared = std::max(lead_shared, cp * block);
+        }
+        spos[lead] = lead_shared;
+      }
+      i = j;
+    }
+  }
+  auto dmode = [&](int s, int lo) { return lo < spos[s] ? kAttnSharedPages : 0; };
   for (int s = 0; s < B; s++) {
     const int n = (int)extents[s], L = (int)lengths[s];
     if (n == 0) continue;
@@ -892,7 +941,7 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       for (int p = 0; p < splits; p++) {
         const int lo = lo0 + p * split, hi = std::min(L, lo + split);
         for (int kvh = 0; kvh < Hkv; kvh++)
-          plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, 0});
+          plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, dmode(s, lo)});
       }
       for (int kvh = 0; kvh < Hkv; kvh++)
         plan.combines.push_back(AttnCombine{s, kvh, 0, n, base + kvh * splits, splits,
@@ -905,13 +954,14 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       // same 2 KiB position rows of the pool at about the same time.
       const int splits = (L + split - 1) / split;
       if (splits <= 1) {
-        for (int kvh = 0; kvh < Hkv; kvh++) plan.items.push_back(AttnItem{s, kvh, 0, n, 0, L, -1, 0});
+        for (int kvh = 0; kvh < Hkv; kvh++)
+          plan.items.push_back(AttnItem{s, kvh, 0, n, 0, L, -1, dmode(s, 0)});
       } else {
         const int base = plan.parts;
         for (int p = 0; p < splits; p++) {
           const int lo = p * split, hi = std::min(L, lo + split);
           for (int kvh = 0; kvh < Hkv; kvh++)
-            plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, 0});
+            plan.items.push_back(AttnItem{s, kvh, 0, n, lo, hi, base + kvh * splits + p, dmode(s, lo)});
         }
         for (int kvh = 0; kvh < Hkv; kvh++)
           plan.combines.push_back(AttnCombine{s, kvh, 0, n, base + kvh * splits, splits, -1, 0, 0, 0});
@@ -951,7 +1001,7 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
   {
     constexpr int kXcd = 8;
     std::vector<AttnItem> pre, dec;
-    for (const AttnItem& x : plan.items) (x.mode ? pre : dec).push_back(x);
+    for (const AttnItem& x : plan.items) ((x.mode & kAttnModeMask) ? pre : dec).push_back(x);
     auto heavy = [](const AttnItem& x, const AttnItem& y) {
       return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
     };
@@ -1040,7 +1090,8 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
   if (!plan.items.empty()) {
     const dim3 grid((unsigned)plan.items.size());
     bool dec = true;
-    for (const AttnItem& x : plan.items) dec = dec && (x.mode == 0 || x.mode == 2);
+    for (const AttnItem& x : plan.items)
+      dec = dec && ((x.mode & kAttnModeMask) == 0 || x.mode == 2);
     if (dec && block == 16 && q_f16) hipLaunchKernelGGL((attn_kernel<16, true, true>), grid, dim3(256), 0, stream, a);
     else if (dec && block == 16) hipLaunchKernelGGL((attn_kernel<16, false, true>), grid, dim3(256), 0, stream, a);
     else if (block == 16 && q_f16) hipLaunchKernelGGL((attn_kernel<16, true>), grid, dim3(256), 0, stream, a);
