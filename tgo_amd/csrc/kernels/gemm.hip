@@ -422,7 +422,7 @@ __device__ __forceinline__ void load_pipeb(const GemmArgs& g, int nb, int ks, in
 // Substep j's B fragment. sz: this wave's scale region of the k-step's stage
 // (scales of block b at b*64 + (2j + h)*8, zeros 128 halves further).
 __device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I4_SYM>& r, int j,
-                                              const half_t* sz, int b, int h) {
+                                              const half_t*, int, int) {
   BRaw<TGOHIP_FORM_I4_SYM> x;
   x.p = r.p;
   x.s = r.s;

@@ -1609,7 +1609,6 @@ int tgohip_sched_submit(tgohip_sched* s, int32_t* out_slot, int32_t* out_done,
     return fail(TGOHIP_ESTATE, "two steps are in flight; collect one before submitting another");
   tgohip_ctx* c = s->ctx;
   const int n = (int)s->slots.size();
-  const tgohip_model_cfg& m = c->cfg;
   std::vector<int32_t> live(n), plen(n), pf(n), ws(n), wst(n), wc(n);
   for (int i = 0; i < n; i++) {
     const SchedSlot& sl = s->slots[i];
