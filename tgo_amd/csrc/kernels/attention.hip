@@ -1006,14 +1006,15 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
     };
     std::stable_sort(dec.begin(), dec.end(), heavy);
-    // Decode items go heavy-first, which keeps the tail short. Beside prefill
-    // items, decode groups (the kv heads of one part) are taken alternately
-    // from the long and the short end: the prefill items' MFMA work then meets
-    // a steady mix of streams. On the C4 step (60 steps, three alternating
-    // pairs on one box) the launch took 0.199-0.201 ms against 0.208-0.218 ms
-    // heavy-first, 5115-5142 against 5009-5081 tok/s. TGOHIP_ATTN_ORDER = 0
-    // keeps heavy-first for every launch.
-    static const int order = [] { const char* e = getenv("TGOHIP_ATTN_ORDER"); return e ? atoi(e) : 1; }();
+    // Decode items go heavy-first, which keeps the tail short. TGOHIP_ATTN_ORDER
+    // = 1 instead takes decode groups (the kv heads of one part) alternately
+    // from the long and the short end beside prefill items, so the prefill
+    // items' MFMA work meets a steady mix of streams: with ordinary K/V loads
+    // that was 2% faster on the C4 step (0.199-0.201 against 0.208-0.218 ms
+    // per launch); with the non-temporal decode loads heavy-first is 0.5%
+    // faster (5218-5283 against 5186-5228 tok/s, five alternating pairs of 60
+    // steps; launch 0.178-0.185 against 0.184-0.189 ms).
+    static const int order = [] { const char* e = getenv("TGOHIP_ATTN_ORDER"); return e ? atoi(e) : 0; }();
     if (order == 1 && !pre.empty() && !dec.empty()) {
       std::vector<std::pair<size_t, size_t>> grp;
       for (size_t i = 0; i < dec.size();) {
