@@ -104,6 +104,29 @@ def test_vocabulary_rows_with_the_maximum_everywhere(ctx, torch_gpu):
     assert mg[-1] == 2.0 ** -20
 
 
+@pytest.mark.parametrize("V", [12291, 8192 + 4])
+def test_rows_split_over_workgroups_at_any_offset(ctx, torch_gpu, V):
+    """A few rows of V logits split over several workgroups each (V odd: element-wise
+    chunks; V % 4 == 0: float4 chunks), with the maximum, its ties, NaNs and +inf placed
+    around every possible chunk edge; against the Go loops."""
+    rng = np.random.default_rng(V)
+    rows = []
+    for edge_frac in (1 / 3, 1 / 2, 2 / 3):
+        e = int(V * edge_frac)
+        for d in (-1, 0, 1):
+            r = list(rng.standard_normal(V).astype(np.float32))
+            r[e + d] = 11.0
+            rows.append(r)
+        r = list(rng.standard_normal(V).astype(np.float32))
+        r[e - 1], r[e], r[e + 1] = 11.0, 11.0, float("nan")
+        rows.append(r)
+        r = list(rng.standard_normal(V).astype(np.float32))
+        r[e + 1] = inf
+        r[0] = nan
+        rows.append(r)
+    check(ctx, torch_gpu, rows)
+
+
 @pytest.mark.parametrize("B", [1, 33, 100, 130, 600])
 def test_batches_of_vocabulary_rows(ctx, torch_gpu, B):
     """B rows of 151936 logits (a row splits over up to 16 workgroups, fewer as B grows):
