@@ -97,6 +97,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+// R > 0: every thread owns at most R float4s of the row (w <= 4 R blockDim.x)
+// and keeps them in registers between the sum of squares and the scaling;
+// R = 0: any width, the second pass reloads the row.
+template <int R>
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t* rows,
                                                        const float* g, int w, float eps,
                                                        void* out, int out_f16, const float* part,
@@ -105,20 +109,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t*
   const int r = blockIdx.x;
   const int step = blockDim.x * 4;
   const size_t src = (size_t)(rows ? rows[r] : (uint32_t)r) * w;
-  float ss = 0.f;
-  for (int i = threadIdx.x * 4; i < w; i += step) {
-    float4_t v = *(const float4_t*)(x + src + i);
-    if (nsplit > 0) {
-      v += sum_planes(part, nsplit, plane, src + i);
-      if (!rows) *(float4_t*)(x + src + i) = v;
-    }
-    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-  }
-  ss = block_sum(ss, red);
-  const float sc = 1.0f / sqrtf(ss / (float)w + eps);
-  for (int i = threadIdx.x * 4; i < w; i += step) {
-    float4_t v = *(const float4_t*)(x + src + i);
-    if (nsplit > 0 && rows) v += sum_planes(part, nsplit, plane, src + i);
+  auto finish = [&](const float4_t& v, int i, float sc) {
     const float4_t gg = *(const float4_t*)(g + i);
     float4_t o;
 #pragma unroll
@@ -128,6 +119,45 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t*
       *(half4_t*)((half_t*)out + (size_t)r * w + i) = hv;
     } else {
       *(float4_t*)((float*)out + (size_t)r * w + i) = o;
+    }
+  };
+  float ss = 0.f;
+  if constexpr (R > 0) {
+    float4_t v[R];
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int i = threadIdx.x * 4 + u * step;
+      if (i >= w) break;
+      v[u] = *(const float4_t*)(x + src + i);
+      if (nsplit > 0) {
+        v[u] += sum_planes(part, nsplit, plane, src + i);
+        if (!rows) *(float4_t*)(x + src + i) = v[u];
+      }
+      ss += v[u][0] * v[u][0] + v[u][1] * v[u][1] + v[u][2] * v[u][2] + v[u][3] * v[u][3];
+    }
+    ss = block_sum(ss, red);
+    const float sc = 1.0f / sqrtf(ss / (float)w + eps);
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int i = threadIdx.x * 4 + u * step;
+      if (i >= w) break;
+      finish(v[u], i, sc);
+    }
+  } else {
+    for (int i = threadIdx.x * 4; i < w; i += step) {
+      float4_t v = *(const float4_t*)(x + src + i);
+      if (nsplit > 0) {
+        v += sum_planes(part, nsplit, plane, src + i);
+        if (!rows) *(float4_t*)(x + src + i) = v;
+      }
+      ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+    ss = block_sum(ss, red);
+    const float sc = 1.0f / sqrtf(ss / (float)w + eps);
+    for (int i = threadIdx.x * 4; i < w; i += step) {
+      float4_t v = *(const float4_t*)(x + src + i);
+      if (nsplit > 0 && rows) v += sum_planes(part, nsplit, plane, src + i);
+      finish(v, i, sc);
     }
   }
 }
@@ -497,8 +527,15 @@ void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, i
                     float eps, void* out, int out_f16, hipStream_t st, const float* part,
                     int nsplit, size_t plane) {
   const int threads = std::min(1024, std::max(64, (w / 4 + 63) / 64 * 64));
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(threads), 0, st, x, rows, g, w, eps, out,
-                     out_f16, part, nsplit, plane);
+  const int per = (w + 4 * threads - 1) / (4 * threads);  // float4s per thread
+#define RMSNORM_LAUNCH(R)                                                                      \
+  hipLaunchKernelGGL(rmsnorm_kernel<R>, dim3(nrows), dim3(threads), 0, st, x, rows, g, w, eps, \
+                     out, out_f16, part, nsplit, plane)
+  if (per <= 1) RMSNORM_LAUNCH(1);
+  else if (per == 2) RMSNORM_LAUNCH(2);
+  else if (per <= 4) RMSNORM_LAUNCH(4);
+  else RMSNORM_LAUNCH(0);
+#undef RMSNORM_LAUNCH
 }
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(derive_rows_kernel, dim3(a.B + 1), dim3(256), 0, st, a);
