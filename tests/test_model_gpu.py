@@ -216,6 +216,35 @@ def test_small_batch_step_on_the_small_m_kernel(torch_gpu, form):
         cpu.close()
 
 
+@pytest.mark.parametrize("hidden", [8192, 16384, 20480])
+def test_wide_hidden_norms(torch_gpu, hidden):
+    """Residual widths past the 8B and 32B shapes (two q heads, so the projections stay
+    small): RMSNorm keeps a thread's 2 (8192) or 4 (16384) float4s of the row in
+    registers between its two passes, and at 20480 (5 per thread) reloads the row; the
+    layer norms and the head's gathered norm, both precisions, against the CPU path."""
+    cfg = dict(layers=1, hidden=hidden, heads=2, kv_heads=1, head_dim=128, ffn=64, vocab=64,
+               eps=1e-6, theta=1e6, block=16, positions=64)
+    for precision in (0, 1):
+        ctx, cpu = make_pair(torch_gpu, cfg, 3, 91 + precision, precision)
+        try:
+            engines = [Engine(b, cfg["vocab"], cfg["heads"], cfg["kv_heads"], cfg["positions"],
+                              cfg["block"], 2) for b in (gpu_backend(ctx), cpu_backend(cpu))]
+            rng = np.random.default_rng(hidden + precision)
+            p0 = [int(t) for t in rng.integers(0, cfg["vocab"], 3)]
+            p1 = [int(t) for t in rng.integers(0, cfg["vocab"], 1)]
+            for e in engines:
+                e.admit(0, p0, 4)
+                e.admit(1, p1, 4)
+            outs = [e.step([(0, p0), (1, p1)]) for e in engines]
+            check_logits(outs[0], outs[1], [0, 1], "prefill %d" % hidden)
+            t0, t1 = argmax_first(outs[1][0]), argmax_first(outs[1][1])
+            outs = [e.step([(0, [t0]), (1, [t1])]) for e in engines]
+            check_logits(outs[0], outs[1], [0, 1], "decode %d" % hidden)
+        finally:
+            ctx.close()
+            cpu.close()
+
+
 @pytest.mark.parametrize("form", [0, 1, 2, 3])
 def test_wide_chunk_step_with_two_k_groups(torch_gpu, form):
     """Qwen3-8B-wide projections at 100 rows (a 96-token chunk beside four decodes): the
