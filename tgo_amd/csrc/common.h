@@ -153,6 +153,7 @@ struct QKRopeArgs {
   int H, Hkv, capacity;
   float eps;
   int q_f16;
+  const float4_t* rope;   // [T][32] (rope_table), or null: the kernel computes the angles
 };
 // ids[t] with bit 31 set names a member b = ids[t] & 0x7fffffff whose token is
 // feed[b] (the previous step's argmax, left on the device).
@@ -175,6 +176,11 @@ struct DeriveArgs {
   uint32_t* slot;  // [T]
 };
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st);
+// table[t * 32 + l] = {cos, sin} of rowpos[t] at the rotary frequencies 2l and
+// 2l + 1 (inv_freq), computed as qk_rope_kv_kernel would: once per step for
+// every layer.
+void launch_rope_table(const uint32_t* rowpos, int T, const double* inv_freq, float4_t* table,
+                       hipStream_t st);
 // keep_idle: members with extent 0 leave out[b] as it is (else out[b] = -1);
 // extents == null: every row is live. margin (nullable): the row's top-two
 // margin in float64 (TopTwoMargin). zero_idle: the logits rows of members with

@@ -211,6 +211,16 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   int cpos = -1;
   float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
   const double inv0 = a.inv_freq[2 * l32], inv1 = a.inv_freq[2 * l32 + 1];
+  if (a.rope) {
+    // the row's angles, computed once per step (the f64 sin and cos per wave
+    // were most of this kernel's time)
+    const float4_t cs = a.rope[(size_t)t * 32 + l32];
+    c0 = cs[0];
+    s0 = cs[1];
+    c1 = cs[2];
+    s1 = cs[3];
+    cpos = dpos;
+  }
   for (int k = wave; 2 * k < NH; k += 4 * gridDim.y) {
     const int hh = 2 * k + half;
     if (hh >= NH) continue;  // an odd head count leaves the last half wave idle
@@ -536,6 +546,21 @@ void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, i
   else if (per <= 4) RMSNORM_LAUNCH(4);
   else RMSNORM_LAUNCH(0);
 #undef RMSNORM_LAUNCH
+}
+__global__ __launch_bounds__(256) void rope_table_kernel(const uint32_t* rowpos, int T,
+                                                        const double* inv_freq, float4_t* table) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // row i / 32, frequency pair i % 32
+  if (i >= T * 32) return;
+  const int l = i & 31;
+  const int pos = (int)rowpos[i >> 5];
+  const double ang0 = (double)pos * inv_freq[2 * l], ang1 = (double)pos * inv_freq[2 * l + 1];
+  table[i] = float4_t{(float)cos(ang0), (float)sin(ang0), (float)cos(ang1), (float)sin(ang1)};
+}
+void launch_rope_table(const uint32_t* rowpos, int T, const double* inv_freq, float4_t* table,
+                       hipStream_t st) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((T * 32 + 255) / 256)), dim3(256), 0, st,
+                     rowpos, T, inv_freq, table);
 }
 void launch_derive_rows(const DeriveArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(derive_rows_kernel, dim3(a.B + 1), dim3(256), 0, st, a);

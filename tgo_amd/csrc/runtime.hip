@@ -142,6 +142,7 @@ struct tgohip_ctx {
   DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, margin, meta, gemm_ws, part_o, part_ml;
   DevBuf amax_part;  // per-chunk partials of the greedy selection
   DevBuf rows;  // [2][rows]: positions and slots derived on the device
+  DevBuf rope;  // [rows][32] float4: the rows' rotary cos and sin (rope_table)
   int rows_cap = 0, batch_cap = 0;
   // pinned staging for per-step metadata
   void* pinned = nullptr;
@@ -449,6 +450,7 @@ int ensure_activations(tgohip_ctx* c, int rows, int B) {
     if ((rc = c->attn.ensure(rows * qw * 4))) return rc;
     if ((rc = c->act.ensure(rows * f * act_el + 256))) return rc;
     if ((rc = c->rows.ensure((size_t)rows * 8))) return rc;
+    if ((rc = c->rope.ensure((size_t)rows * 32 * sizeof(float4_t)))) return rc;
     c->rows_cap = rows;
   }
   if (B > c->batch_cap) {
@@ -535,7 +537,7 @@ void tgohip_close(tgohip_ctx* c) {
   c->allocs.clear();
   for (DevBuf* b : {&c->h, &c->xn, &c->qkv, &c->q, &c->attn, &c->act, &c->lastn, &c->logits,
                     &c->argmax, &c->margin, &c->amax_part, &c->meta, &c->gemm_ws, &c->part_o, &c->part_ml,
-                    &c->rows})
+                    &c->rows, &c->rope})
     b->release();
   if (c->kc) (void)hipFree(c->kc);
   if (c->vc) (void)hipFree(c->vc);
@@ -959,10 +961,12 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
   uint32_t* d_rowpos = (uint32_t*)c->rows.p;
   uint32_t* d_rowslot = d_rowpos + T;
-  if (derived)
+  if (derived) {
     launch_derive_rows(DeriveArgs{dp.cu, dp.lengths, d_ext, dp.pages, B, s->max_pages, m.block,
                                   plan.claimed, pad, T, c->kv_positions, d_rowpos, d_rowslot},
                        st);
+    launch_rope_table(d_rowpos, T, c->inv_freq, (float4_t*)c->rope.p, st);
+  }
   // A split-K projection's partial planes are summed by the kernel that reads
   // its output next (in split order, so the result is the reduction's):
   // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
@@ -984,7 +988,8 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
-                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16};
+                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16,
+                  derived ? (const float4_t*)c->rope.p : nullptr};
     launch_qk_rope_kv(qa, T, st);
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 0))) return rc;
     if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
