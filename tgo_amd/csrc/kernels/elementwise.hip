@@ -7,6 +7,8 @@
 //   qk_rope_kv_kernel   q/k RMSNorm per head + interleaved RoPE + f16 narrowing +
 //                       ScatterRows into the paged pool, slot >= capacity dropped
 //                       (nn/attention.go:192-232, plan.go:182-192)
+//   rope_table_kernel   the rows' rotary cos and sin (nn/attention.go:203-211),
+//                       once per step for every layer's qk_rope_kv_kernel
 //   argmax_*_kernel     greedy token, first strict maximum (sample/stages.go:196),
 //                       and the top-two margin
 //   synth_* kernels     seeded random-init weights, bit-identical to the CPU
