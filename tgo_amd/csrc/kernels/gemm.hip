@@ -208,7 +208,10 @@ __device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I8>& r, int j) {
   return deq_i8(w0, w1, s.h);
 }
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) (nn/blocks.go:62-66) with the hardware reciprocal
+// (v_rcp_f32, 1 ulp) in place of the IEEE division's ten-instruction sequence:
+// the SwiGLU epilogue of the C4 gate/up 209 -> 205 us.
+__device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
 
 // 16-byte slot of (row, k-chunk) in an LDS activation tile of 8 chunks per row.
 // The XOR with (row/2) % 8 spreads any 16 consecutive rows of one k-chunk over
