@@ -4,7 +4,9 @@ the device, and overlap mode (submit / collect) against the synchronous step.
 * A step whose posq, posk and slots are left to the device gives the same
   logits, to the bit, as the same step with NewBatchStep's packed ports
   (model.NewBatchStep, batch.go:310-340, restated in oracle/host.py), padding
-  rows included.
+  rows included. The derived rows also take their rotary cos and sin from the
+  table computed once per step, the packed ports from the angles computed in
+  the q/k-norm + RoPE kernel: the two agree to the bit.
 * Overlap mode runs the steps the synchronous scheduler runs when the caller
   admits and retires the same sequences before each submit as before each
   step. Each sequence's greedy tokens are then identical: a row's result does
