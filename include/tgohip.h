@@ -164,7 +164,12 @@ typedef struct {
  * b with cu_b <= t (cu: prefix sums of extents) and sits at position
  * p = lengths[b] - extents[b] + (t - cu_b), slot pages[b][p / block] * block +
  * p % block; rows past sum(extents) repeat the last member's last position
- * with slot = capacity. Only ids and the per-member ports then cross PCIe. */
+ * with slot = capacity. Only ids and the per-member ports then cross PCIe.
+ * Padding rows (t >= sum(extents), a bucket's rows: batch.go:362-366) are not
+ * computed when they cannot change anything: every padding row's slot is at
+ * or past capacity (its K/V write is dropped, plan.go:180-192) and no member
+ * with a nonzero extent reads its logits from one. A step bucketed from 1152
+ * to 2048 rows then costs the 1152 rows. Otherwise every row runs. */
 int tgohip_step(tgohip_ctx* ctx, const tgohip_batch_step* step, float* logits_out,
                 int32_t* argmax_out, tgohip_timings* timings);
 
@@ -230,6 +235,10 @@ int tgohip_linear(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M
  * two contexts at once) race; calls in stream order do not. */
 int tgohip_linear_noalloc(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M,
                           void* y, int y_dtype);
+/* Bytes of split-K partials a linear call over M rows of a handle's weight
+ * with f16 (x_dtype TGOHIP_F16) or f32 activations needs: 0 when it runs
+ * unsplit. tgohip_linear_noalloc refuses calls above 64 MiB. */
+int tgohip_linear_workspace(tgohip_ctx* ctx, int handle, int x_dtype, int M, size_t* bytes);
 
 /* Dequantizes a handle's weight to f32 [K,N] on the device exactly as the
  * host restatement does ((q - z) * s in f32). y: device [K,N] f32. */

@@ -1,9 +1,9 @@
 """tgohip_linear_noalloc -- the linear whose split-K partials live in the library's
 static device workspace -- against tgohip_linear, through the C ABI: the same kernels and
 splits, so the outputs are equal to the bit. Two calls in a row, the second with fewer
-rows, so the second runs on the array the first left behind; shapes where split-K runs
-(the workspace is used) and where it does not; a call needing more than the array holds is
-refused."""
+rows, so the second runs on the array the first left behind; every call here splits K
+(tgohip_linear_workspace says so), so both use the array; an empty batch launches nothing;
+a call needing more than the array holds is refused."""
 import numpy as np
 import pytest
 
@@ -18,11 +18,11 @@ def weight(ctx, form, K, N, seed):
 
 
 @pytest.mark.parametrize("form,K,N,Ms,xf", [
-    (tgo_amd.FORM_I4_SYM, 12288, 4096, (256, 1), tgo_amd.F16),   # pipe kernel 8 splits, then gemm_kernel 32
+    (tgo_amd.FORM_I4_SYM, 12288, 4096, (256, 40), tgo_amd.F16),   # pipelined kernel, 8 splits both
     (tgo_amd.FORM_I4_SYM, 12288, 4096, (1024, 512), tgo_amd.F16),  # 4 then 8 splits, 64 MiB each
-    (tgo_amd.FORM_I8, 4096, 6144, (64, 8), tgo_amd.F16),
+    (tgo_amd.FORM_I8, 4096, 6144, (64, 48), tgo_amd.F16),          # 8 splits both
     (tgo_amd.FORM_F16, 4096, 4096, (200, 33), tgo_amd.F32),       # gemm_kernel, 16 splits, f32 x
-    (tgo_amd.FORM_I4_TGO, 4096, 12288, (130, 1), tgo_amd.F16),
+    (tgo_amd.FORM_I4_TGO, 4096, 12288, (130, 65), tgo_amd.F16),    # 3 then 4 splits
 ])
 def test_noalloc_linear_equals_linear(ctx, torch_gpu, form, K, N, Ms, xf):
     torch = torch_gpu
@@ -30,6 +30,7 @@ def test_noalloc_linear_equals_linear(ctx, torch_gpu, form, K, N, Ms, xf):
     try:
         for M in Ms:
             print("no-alloc linear: form %d [%d,%d] M=%d" % (form, K, N, M), flush=True)
+            assert ctx.linear_workspace(h, M, x_dtype=xf) > 0, "this call should split K"
             g = torch.Generator(device="cuda").manual_seed(M)
             x = torch.randn(M, K, device="cuda", generator=g)
             x = x.half() if xf == tgo_amd.F16 else x
@@ -55,5 +56,22 @@ def test_noalloc_linear_refuses_beyond_its_workspace(ctx, torch_gpu):
             ctx.linear_noalloc(h, x, 2100, y)
         ctx.linear_noalloc(h, x, 2000, y)  # two planes of 32 MiB fit
         torch.cuda.synchronize()
+    finally:
+        ctx.weight_free(h)
+
+
+def test_noalloc_linear_empty_batch_launches_nothing(ctx, torch_gpu):
+    """M = 0 (an empty batch in a serving loop): both linear entry points return at once,
+    with nothing written and no split-K arithmetic over zero tiles."""
+    torch = torch_gpu
+    h = weight(ctx, tgo_amd.FORM_I4_SYM, 4096, 6144, 9)
+    try:
+        assert ctx.linear_workspace(h, 0, x_dtype=tgo_amd.F16) == 0
+        x = torch.zeros(1, 4096, device="cuda").half()
+        y = torch.full((1, 6144), 7.0, device="cuda")
+        ctx.linear(h, x, 0, y, x_dtype=tgo_amd.F16)
+        ctx.linear_noalloc(h, x, 0, y, x_dtype=tgo_amd.F16)
+        torch.cuda.synchronize()
+        assert bool((y == 7.0).all())
     finally:
         ctx.weight_free(h)

@@ -85,6 +85,7 @@ def lib():
         "tgohip_weight_free": (I, [P, I]),
         "tgohip_linear": (I, [P, I, P, I, I, P, I]),
         "tgohip_linear_noalloc": (I, [P, I, P, I, I, P, I]),
+        "tgohip_linear_workspace": (I, [P, I, I, I, P]),
         "tgohip_dequant": (I, [P, I, P]),
         "tgohip_dequant_f16": (I, [P, I, P]),
         "tgohip_greedy": (I, [P, P, I, I, P, P]),
@@ -586,6 +587,12 @@ class Context:
     def linear_noalloc(self, handle, x, M, y, x_dtype=F32, y_dtype=F32):
         """linear with its split-K partials in the library's static workspace."""
         check(lib().tgohip_linear_noalloc(self.h, handle, ptr(x), x_dtype, M, ptr(y), y_dtype))
+
+    def linear_workspace(self, handle, M, x_dtype=F32):
+        """Bytes of split-K partials a linear call over M rows uses (0: unsplit)."""
+        n = ctypes.c_size_t()
+        check(lib().tgohip_linear_workspace(self.h, handle, x_dtype, M, ctypes.byref(n)))
+        return n.value
 
     def dequant(self, handle, y):
         check(lib().tgohip_dequant(self.h, handle, ptr(y)))

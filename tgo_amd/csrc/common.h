@@ -101,7 +101,10 @@ size_t packed_scale_halves(int form, int K, int N);
 int repack_enqueue(int form, const void* plane, const uint16_t* scales, const uint16_t* zeros,
                    int K, int N, PackedWeight& w, int nb_stride, int nb_off, hipStream_t st);
 int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t st);
-size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu);
+// Split-K workspace of a call: x_f32 < 0 bounds every activation type and
+// epilogue; 0/1 gives exactly what an f32/f16-epilogue call over f16/f32
+// activations uses.
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int x_f32 = -1);
 // With defer != nullptr a split-K launch leaves its partial planes in the
 // workspace ([splits][M][N] f32) and sets *defer = splits instead of running
 // the reduction; the caller folds them into the consumer (rmsnorm,

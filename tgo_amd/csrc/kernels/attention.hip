@@ -425,12 +425,15 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           m = mnew;
         }
         float psum = 0.f;
-        half4_t pb;
+        half4_t pb, pl;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const float p = __builtin_amdgcn_exp2f(fmaf(st[q], qs, -m));
           psum += p;
           pb[q] = (half_t)p;
+          // f32 q (tgo's arithmetic): P as f16 hi + lo, so V is weighted by
+          // the f32 probability the normalizer l sums
+          if (!QF16) pl[q] = (half_t)(p - (float)pb[q]);
         }
         psum = wave_sum16x(psum);
         l += psum;
@@ -440,6 +443,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
           for (int db = 0; db < 8; db++) {
             const half4_t va = attn_vt4(Vw, 4 * lg, db * 16, li);
             o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[db], 0, 0, 0);
+            if (!QF16) o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, o[db], 0, 0, 0);
           }
         }
       }
@@ -592,14 +596,16 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
       m = mnew;
     }
     float psum = 0.f;
-    half8_t pf[2][2];
+    half8_t pf[2][2], pfl[2][2];
 #pragma unroll
     for (int pb = 0; pb < 2; pb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const float p = __builtin_amdgcn_exp2f(fmaf(sc[pb][i], qs, -m));
         psum += p;
-        pf[pb][i >> 3][i & 7] = (half_t)p;
+        const half_t ph = (half_t)p;
+        pf[pb][i >> 3][i & 7] = ph;
+        if (!QF16) pfl[pb][i >> 3][i & 7] = (half_t)(p - (float)ph);  // P as hi + lo (f32 q)
       }
     psum += __shfl_xor(psum, 32, 64);
     l += psum;
@@ -618,6 +624,7 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
           const half4_t v1 = attn_vt4(Vs, p0 + 8, db * 32 + dgrp, j16);
           const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[pb][t], o[db], 0, 0, 0);
+          if (!QF16) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pfl[pb][t], o[db], 0, 0, 0);
         }
       }
   }
@@ -664,9 +671,10 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
 // DEC: a launch of decode-style items only (a decode-only step). Without the
 // prefill path the kernel fits 128 VGPRs instead of 218, so four workgroups
 // share a CU instead of two: the C4 decode-only step's attention launch
-// 0.1634-0.1638 -> 0.1622-0.1624 ms (three alternating pairs).
+// 0.1634-0.1638 -> 0.1622-0.1624 ms (three alternating pairs). With an f32
+// query (q and P as hi + lo) it needs 152 and three share a CU.
 template <int BLK, bool QF16, bool DEC = false>
-__global__ __launch_bounds__(256, DEC ? 4 : 2) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, DEC ? (QF16 ? 4 : 3) : 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmem];
   const AttnItem it = a.items[blockIdx.x];
   if (it.mode == 2) return;  // an empty slot of the XCD-aware order

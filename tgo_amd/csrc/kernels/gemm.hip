@@ -208,6 +208,92 @@ __device__ __forceinline__ half8_t bfrag(const BRaw<TGOHIP_FORM_I8>& r, int j) {
   return deq_i8(w0, w1, s.h);
 }
 
+// ---- exact dequantized weights as two f16 fragments ------------------------
+// hi = RNE_f16((q - z) * s) and lo = (q - z) * s - hi, each f16, so hi + lo is
+// the exact product tgo's CPU path multiplies (the f32 dequantization): (q - z)
+// has at most 8 significant bits and s 11, so the residual after hi's 11 bits
+// fits lo's (down to f16's subnormal spacing, 2^-24). lo comes from one fused
+// multiply-add, q*s - hi, rounded once and exact. An MFMA with each half gives
+// the product against the unrounded weight.
+__device__ __forceinline__ void split_pair(half2_t d, half2_t s2, half2_t& hi, half2_t& lo) {
+  hi = d * s2;
+  lo = __builtin_elementwise_fma(d, s2, -hi);
+}
+__device__ __forceinline__ void pack_pair(half8_t& o, int j, half2_t h) {
+  o[2 * j] = h[0];
+  o[2 * j + 1] = h[1];
+}
+template <int FORM>
+__device__ __forceinline__ void bfrag_split(const BRaw<FORM>& r, int j, half8_t& hi, half8_t& lo);
+template <>
+__device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I4_SYM>& r, int j, half8_t& hi,
+                                            half8_t& lo) {
+  union { uint32_t u; half2_t h; } sc;
+  sc.u = r.s;
+  const half_t s = j < 2 ? sc.h[0] : sc.h[1];
+  const half2_t sp = {s, s};
+  const uint32_t w = word_of(r.p, j), w8 = w >> 8;
+  const half2_t b0 = {(half_t)1032.f, (half_t)1032.f}, b1 = {(half_t)72.f, (half_t)72.f};
+  // q - 8 exactly, as in deq_i4_sym
+  const half2_t d[4] = {as_h2((w & 0x000F000Fu) | 0x64006400u) - b0,
+                        as_h2((w & 0x00F000F0u) | 0x54005400u) - b1,
+                        as_h2((w8 & 0x000F000Fu) | 0x64006400u) - b0,
+                        as_h2((w8 & 0x00F000F0u) | 0x54005400u) - b1};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    half2_t h, l;
+    split_pair(d[i], sp, h, l);
+    pack_pair(hi, i, h);
+    pack_pair(lo, i, l);
+  }
+}
+template <>
+__device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I4_TGO>& r, int j, half8_t& hi,
+                                            half8_t& lo) {
+  U16B s, z;
+  s.u = r.s[j];
+  z.u = r.z[j];
+  const uint32_t w = word_of(r.p, j);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    // (1024 + q) - (1024 + z) = q - z exactly
+    const half2_t d = as_h2(((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u) -
+                      half2_t{z.h[2 * i], z.h[2 * i + 1]};
+    half2_t h, l;
+    split_pair(d, half2_t{s.h[2 * i], s.h[2 * i + 1]}, h, l);
+    pack_pair(hi, i, h);
+    pack_pair(lo, i, l);
+  }
+}
+template <>
+__device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I8>& r, int j, half8_t& hi,
+                                            half8_t& lo) {
+  const uint4 q = r.p[j >> 1];
+  const uint32_t ws[2] = {(j & 1) ? q.z : q.x, (j & 1) ? q.w : q.y};
+  U16B s;
+  s.u = r.s[j];
+  const half2_t bias = {(half_t)1152.f, (half_t)1152.f};
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    // (1024 + q + 128) - 1152 = q exactly
+    const half2_t dl = as_h2((ws[u] & 0x00FF00FFu) | 0x64006400u) - bias;
+    const half2_t dh = as_h2(((ws[u] >> 8) & 0x00FF00FFu) | 0x64006400u) - bias;
+    half2_t h, l;
+    split_pair(dl, half2_t{s.h[4 * u], s.h[4 * u + 1]}, h, l);
+    pack_pair(hi, 2 * u, h);
+    pack_pair(lo, 2 * u, l);
+    split_pair(dh, half2_t{s.h[4 * u + 2], s.h[4 * u + 3]}, h, l);
+    pack_pair(hi, 2 * u + 1, h);
+    pack_pair(lo, 2 * u + 1, l);
+  }
+}
+template <>
+__device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_F16>& r, int j, half8_t& hi,
+                                            half8_t& lo) {
+  hi = bfrag(r, j);  // f16 weights are exact as stored
+  lo = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+}
+
 // silu(g) = g / (1 + e^-g) (nn/blocks.go:62-66) with the hardware reciprocal
 // (v_rcp_f32, 1 ulp) in place of the IEEE division's ten-instruction sequence:
 // the SwiGLU epilogue of the C4 gate/up 209 -> 205 us.
@@ -267,10 +353,16 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ASPLIT (f32 activations, tgo's arithmetic): the activation is carried as f16
+// hi + lo (about 22 bits) and the quantized weights as their exact hi + lo
+// (bfrag_split), three MFMAs per product (hi.hi, lo.hi, hi.lo; lo.lo is below
+// f32 rounding): the product of the f32 activation and the unrounded
+// dequantized weight, f32 accumulated, as tgo's CPU path computes it.
 template <int FORM, int MW, bool ASPLIT, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   constexpr int MB = MW / 32;
   constexpr int APLANES = ASPLIT ? 2 : 1;
+  constexpr bool BSPLIT = ASPLIT && FORM != TGOHIP_FORM_F16;
   __shared__ __attribute__((aligned(16))) half_t As[2][APLANES][MW * 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -354,9 +446,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      half8_t bf[2];
+      half8_t bf[2], bl[2];
 #pragma unroll
-      for (int b = 0; b < 2; b++) bf[b] = bfrag(bcur[b], j);
+      for (int b = 0; b < 2; b++) {
+        if constexpr (BSPLIT) bfrag_split(bcur[b], j, bf[b], bl[b]);
+        else bf[b] = bfrag(bcur[b], j);
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; mb++) {
         const int row = mb * 32 + c32;
@@ -366,8 +461,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         for (int p = 0; p < APLANES; p++) {
           const half8_t af = ((const half8_t*)As[buf][p])[phys];
 #pragma unroll
-          for (int b = 0; b < 2; b++)
+          for (int b = 0; b < 2; b++) {
             acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[b], acc[mb][b], 0, 0, 0);
+            if (BSPLIT && p == 0)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bl[b], acc[mb][b], 0, 0, 0);
+          }
         }
       }
     }
@@ -1284,7 +1382,7 @@ static int pipe_max_splits() {
 }
 
 static int choose_pipe_splits(int tiles, int KS, int slots) {
-  if (tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
+  if (tiles <= 0 || tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
   int s = slots / tiles;              // one round of workgroups
   while (s > 1 && KS / s < 8) s--;
   return std::max(1, std::min(s, pipe_max_splits()));
@@ -1324,15 +1422,6 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
   if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) && tiles >= ncu / 2) splits = 1;
 }
 
-// Workspace bytes a call needs for split-K partials.
-size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu) {
-  const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
-  int s = choose_splits(M, w.N, w.K, MW, ncu);
-  int mw, nw, tiles_n, tiles, ps;
-  pipe_shape(w, M, ncu, mw, nw, tiles_n, tiles, ps);
-  s = std::max(s, ps);
-  return s > 1 ? (size_t)s * split_plane_stride(M, w.N) * sizeof(float) : 0;
-}
 
 template <int FORM, int MW, int NW, int KQ = 1>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
@@ -1365,10 +1454,32 @@ static bool pipe_kq_enabled() {
   return v;
 }
 
+// The pipelined kernel's launch: tile shape, k groups, k-steps per split and
+// the split count those give.
+struct PipeLaunch {
+  int mw, nw, tiles_n, tiles, splits, kq, ksteps_per_split;
+};
+static PipeLaunch pipe_launch(const PackedWeight& w, int M, int ncu, int epi) {
+  PipeLaunch p;
+  pipe_shape(w, M, ncu, p.mw, p.nw, p.tiles_n, p.tiles, p.splits, epi);
+  const int KS = w.K / 64;
+  // Two k groups per workgroup (KQ = 2) where unsplit 64-row tiles would put
+  // at most one wave on each SIMD (at most one workgroup per CU): the SwiGLU
+  // gate/up of a 128-row step, 38.3 -> 35.6 us. Split projections keep one
+  // group (O and down at 128 rows, 8 splits of 8 and 24 k-steps, ran 6% and
+  // 2% slower with two).
+  p.kq = (p.mw == 64 && p.splits == 1 && p.tiles <= ncu && KS % 8 == 0 && pipe_kq_enabled()) ? 2 : 1;
+  // whole groups of 4 k-steps per split and k group (KS is a multiple of 4)
+  p.ksteps_per_split = ((KS + p.splits - 1) / p.splits + 4 * p.kq - 1) / (4 * p.kq) * (4 * p.kq);
+  p.splits = (KS + p.ksteps_per_split - 1) / p.ksteps_per_split;
+  return p;
+}
+
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
                              float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
-  int mw, nw, tiles_n, tiles, splits;
-  pipe_shape(w, M, ncu, mw, nw, tiles_n, tiles, splits, epi);
+  const PipeLaunch pl = pipe_launch(w, M, ncu, epi);
+  const int mw = pl.mw, nw = pl.nw, tiles_n = pl.tiles_n, tiles = pl.tiles, kq = pl.kq;
+  int splits = pl.splits;
   GemmArgs g{};
   g.x = x;
   g.wp = w.wp;
@@ -1378,16 +1489,7 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
   g.M = M;
   g.K = w.K;
   g.N = w.N;
-  const int KS = w.K / 64;
-  // Two k groups per workgroup (KQ = 2) where unsplit 64-row tiles would put
-  // at most one wave on each SIMD (at most one workgroup per CU): the SwiGLU
-  // gate/up of a 128-row step, 38.3 -> 35.6 us. Split projections keep one
-  // group (O and down at 128 rows, 8 splits of 8 and 24 k-steps, ran 6% and
-  // 2% slower with two).
-  const int kq = (mw == 64 && splits == 1 && tiles <= ncu && KS % 8 == 0 && pipe_kq_enabled()) ? 2 : 1;
-  // whole groups of 4 k-steps per split and k group (KS is a multiple of 4)
-  g.ksteps_per_split = ((KS + splits - 1) / splits + 4 * kq - 1) / (4 * kq) * (4 * kq);
-  splits = (KS + g.ksteps_per_split - 1) / g.ksteps_per_split;
+  g.ksteps_per_split = pl.ksteps_per_split;
   if (splits > 1) {
     if (!workspace || ws_bytes < (size_t)splits * split_plane_stride(M, w.N) * sizeof(float))
       return fail(TGOHIP_ESTATE, "linear: split-K workspace too small");
@@ -1436,6 +1538,25 @@ static int pipe_min_rows() {
 static bool use_pipe(const PackedWeight& w, bool x_f32, int M) {
   return !x_f32 && w.form != TGOHIP_FORM_F16 && M >= pipe_min_rows() && (w.K / 64) % 4 == 0 &&
          (int64_t)M * w.K < ((int64_t)1 << 31);  // its activation offsets are 32-bit
+}
+
+// Workspace bytes a call needs for split-K partials: x_f32 < 0 bounds every
+// activation type and epilogue; otherwise the bytes of exactly the call
+// gemm_enqueue makes with an f32 or f16 epilogue.
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int x_f32) {
+  if (M <= 0) return 0;  // nothing launches (and no tiles to divide the slots by)
+  const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
+  int s;
+  if (x_f32 < 0) {
+    s = std::max(choose_splits(M, w.N, w.K, MW, ncu), pipe_launch(w, M, ncu, EPI_F32).splits);
+  } else if (use_pipe(w, x_f32 != 0, M)) {
+    s = pipe_launch(w, M, ncu, EPI_F32).splits;
+  } else if (use_gemv(w, x_f32 != 0, M, ncu)) {
+    s = 1;
+  } else {
+    s = choose_splits(M, w.N, w.K, MW, ncu);  // gemm_kernel's grid.z
+  }
+  return s > 1 ? (size_t)s * split_plane_stride(M, w.N) * sizeof(float) : 0;
 }
 
 int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,

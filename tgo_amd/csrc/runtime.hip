@@ -144,6 +144,7 @@ struct tgohip_ctx {
   DevBuf rows;  // [2][rows]: positions and slots derived on the device
   DevBuf rope;  // [rows][32] float4: the rows' rotary cos and sin (rope_table)
   int rows_cap = 0, batch_cap = 0;
+  int last_batch = 0;  // members of the last launched step (its margins are in `margin`)
   // pinned staging for per-step metadata
   void* pinned = nullptr;
   size_t pinned_bytes = 0;
@@ -883,15 +884,32 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   if (derived && pad < 0)
     return fail(TGOHIP_EINVAL, "step: every member contributes nothing; there are no positions "
                                "to derive");
-  if ((rc = ensure_activations(c, T, B))) return rc;
+  // Rows past the members' (sum of extents) are a bucket's padding
+  // (batch.go:362-366, model/batch.go:140-150): attention leaves them inert,
+  // no member reads their logits, and a slot at or past capacity drops their
+  // K/V write (plan.go:180-192). Such rows change nothing, so the step runs
+  // over the members' rows only: a 1152-row step bucketed to 2048 costs what
+  // the 1152 rows cost. A padding row whose slot is in the pool (ports not
+  // packed by NewBatchStep) would write K/V, and a member reading its logits
+  // from a padding row needs it computed: then every row runs.
+  int Tw = T;
+  if (plan.claimed > 0 && plan.claimed < T) {
+    bool inert = true;
+    if (!derived)
+      for (int t = plan.claimed; t < T && inert; t++) inert = s->slots[t] >= (uint32_t)c->kv_positions;
+    for (int b = 0; b < B && inert; b++)
+      if (s->extents[b] > 0 && s->last[b] >= (uint32_t)plan.claimed) inert = false;
+    if (inert) Tw = plan.claimed;
+  }
+  if ((rc = ensure_activations(c, Tw, B))) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
 
   // One staged upload of every port (batch.go:385-405).
   Stager sg;
-  const size_t o_ids = sg.add(s->ids, (size_t)T * 4);
-  const size_t o_posq = derived ? 0 : sg.add(s->posq, (size_t)T * m.heads * 4);
-  const size_t o_posk = derived ? 0 : sg.add(s->posk, (size_t)T * m.kv_heads * 4);
-  const size_t o_slots = derived ? 0 : sg.add(s->slots, (size_t)T * 4);
+  const size_t o_ids = sg.add(s->ids, (size_t)Tw * 4);
+  const size_t o_posq = derived ? 0 : sg.add(s->posq, (size_t)Tw * m.heads * 4);
+  const size_t o_posk = derived ? 0 : sg.add(s->posk, (size_t)Tw * m.kv_heads * 4);
+  const size_t o_slots = derived ? 0 : sg.add(s->slots, (size_t)Tw * 4);
   const size_t o_len = sg.add(s->lengths, (size_t)B * 4);
   const size_t o_ext = sg.add(s->extents, (size_t)B * 4);
   const size_t o_last = sg.add(s->last, (size_t)B * 4);
@@ -936,11 +954,11 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     ab -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
     o.prof.flops[TGOHIP_PROF_ATTN] = 4.0 * kHeadDim * m.heads * pairs;
     const Layer& L0 = c->layers[0];
-    gemm_algorithmic(L0.qkv, T, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_QKV], o.prof.flops[TGOHIP_PROF_QKV]);
-    gemm_algorithmic(L0.wo, T, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_O], o.prof.flops[TGOHIP_PROF_O]);
-    gemm_algorithmic(L0.gateup, T, f32act, f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16,
+    gemm_algorithmic(L0.qkv, Tw, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_QKV], o.prof.flops[TGOHIP_PROF_QKV]);
+    gemm_algorithmic(L0.wo, Tw, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_O], o.prof.flops[TGOHIP_PROF_O]);
+    gemm_algorithmic(L0.gateup, Tw, f32act, f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16,
                      o.prof.bytes[TGOHIP_PROF_GATEUP], o.prof.flops[TGOHIP_PROF_GATEUP]);
-    gemm_algorithmic(L0.down, T, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
+    gemm_algorithmic(L0.down, Tw, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
     gemm_algorithmic(c->lm_head, B, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
                      o.prof.flops[TGOHIP_PROF_LMHEAD]);
     while (c->prof_ev.size() < (size_t)2 * m.layers * NK * 2) {
@@ -958,56 +976,56 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
       TGOHIP_HIP(hipEventRecord(pev[((size_t)l * NK + kind) * 2 + end], st));
     return 0;
   };
-  launch_embed(d_ids, T, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
+  launch_embed(d_ids, Tw, c->embed, c->embed_scales, c->embed_form, m.hidden, h, st, o.feed);
   uint32_t* d_rowpos = (uint32_t*)c->rows.p;
-  uint32_t* d_rowslot = d_rowpos + T;
+  uint32_t* d_rowslot = d_rowpos + Tw;
   if (derived) {
     launch_derive_rows(DeriveArgs{dp.cu, dp.lengths, d_ext, dp.pages, B, s->max_pages, m.block,
-                                  plan.claimed, pad, T, c->kv_positions, d_rowpos, d_rowslot},
+                                  plan.claimed, pad, Tw, c->kv_positions, d_rowpos, d_rowslot},
                        st);
-    launch_rope_table(d_rowpos, T, c->inv_freq, (float4_t*)c->rope.p, st);
+    launch_rope_table(d_rowpos, Tw, c->inv_freq, (float4_t*)c->rope.p, st);
   }
   // A split-K projection's partial planes are summed by the kernel that reads
   // its output next (in split order, so the result is the reduction's):
   // QKV's by qk_rope_kv, O's and down's (residual adds) by the following
   // rmsnorm. `pend` counts the planes of a residual add still owed to h.
-  const size_t plane = split_plane_stride(T, m.hidden);
+  const size_t plane = split_plane_stride(Tw, m.hidden);
   int pend = 0;
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
-    launch_rmsnorm(h, nullptr, T, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    launch_rmsnorm(h, nullptr, Tw, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
     int qkv_split = 0;
     if ((rc = mark(TGOHIP_PROF_QKV, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, T, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
+    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, Tw, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
                            &qkv_split)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
     QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
-                  split_plane_stride(T, (m.heads + 2 * m.kv_heads) * kHeadDim), L.g_q, L.g_k,
+                  split_plane_stride(Tw, (m.heads + 2 * m.kv_heads) * kHeadDim), L.g_q, L.g_k,
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16,
                   derived ? (const float4_t*)c->rope.p : nullptr};
-    launch_qk_rope_kv(qa, T, st);
+    launch_qk_rope_kv(qa, Tw, st);
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 0))) return rc;
     if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
-                           actf16, T, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
+                           actf16, Tw, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 1))) return rc;
     if ((rc = mark(TGOHIP_PROF_O, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
+    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_O, l, 1))) return rc;
-    launch_rmsnorm(h, nullptr, T, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    launch_rmsnorm(h, nullptr, Tw, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
     if ((rc = mark(TGOHIP_PROF_GATEUP, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, T, c->act.p,
+    if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, Tw, c->act.p,
                            f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_GATEUP, l, 1))) return rc;
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, T, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
+    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 1))) return rc;
   }
@@ -1023,6 +1041,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                 o.keep_idle, (double*)c->margin.p, 1);
   TGOHIP_HIP(hipEventRecord(o.ev_end, st));
   TGOHIP_HIP(hipGetLastError());
+  c->last_batch = B;
   return 0;
 }
 
@@ -1082,9 +1101,9 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
 // The top-two margins of the last step's members (TopTwoMargin,
 // internal/conformance/measure.go:91), waiting for the step to land.
 int tgohip_step_margins(tgohip_ctx* c, double* out, int B) {
-  if (B <= 0 || B > c->batch_cap || !c->margin.p)
+  if (B <= 0 || B > c->last_batch || !c->margin.p)
     return fail(TGOHIP_EINVAL, "step margins: " + std::to_string(B) + " members asked and the last "
-                               "step held at most " + std::to_string(c->batch_cap));
+                               "step held " + std::to_string(c->last_batch));
   TGOHIP_HIP(hipStreamSynchronize(c->stream));
   TGOHIP_HIP(hipMemcpy(out, c->margin.p, (size_t)B * 8, hipMemcpyDeviceToHost));
   return 0;
@@ -1226,6 +1245,8 @@ static PackedWeight* handle_of(tgohip_ctx* c, int handle) {
 int tgohip_linear(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, void* y, int y_dtype) {
   PackedWeight* w = handle_of(c, handle);
   if (!w) return TGOHIP_EINVAL;
+  if (M < 0) return fail(TGOHIP_EINVAL, "linear: M is " + std::to_string(M));
+  if (M == 0) return 0;  // an empty batch: nothing to launch
   const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
   int rc = c->gemm_ws.ensure(ws + 256);
   if (rc) return rc;
@@ -1241,6 +1262,7 @@ int tgohip_linear_noalloc(tgohip_ctx* c, int handle, const void* x, int x_dtype,
   PackedWeight* w = handle_of(c, handle);
   if (!w) return TGOHIP_EINVAL;
   if (M < 0) return fail(TGOHIP_EINVAL, "linear_noalloc: M is " + std::to_string(M));
+  if (M == 0) return 0;  // an empty batch: nothing to launch
   const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
   if (ws > kScratchBytes)
     return fail(TGOHIP_EINVAL, "linear_noalloc: M = " + std::to_string(M) + " over [" +
@@ -1251,6 +1273,14 @@ int tgohip_linear_noalloc(tgohip_ctx* c, int handle, const void* x, int x_dtype,
   if (!c->scratch) return fail(TGOHIP_ESTATE, "linear_noalloc: no workspace address for this device");
   return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
                       (float*)c->scratch, kScratchBytes, c->ncu, c->stream);
+}
+
+int tgohip_linear_workspace(tgohip_ctx* c, int handle, int x_dtype, int M, size_t* bytes) {
+  PackedWeight* w = handle_of(c, handle);
+  if (!w) return TGOHIP_EINVAL;
+  if (M < 0) return fail(TGOHIP_EINVAL, "linear_workspace: M is " + std::to_string(M));
+  *bytes = gemm_workspace_bytes(*w, M, c->ncu, x_dtype == TGOHIP_F32);
+  return 0;
 }
 
 int tgohip_dequant(tgohip_ctx* c, int handle, float* y) {
