@@ -55,6 +55,10 @@ extern "C" {
 /* Activation / output dtypes */
 #define TGOHIP_F32 0
 #define TGOHIP_F16 1
+/* An f32 activation [M,K] already split for tgo's arithmetic (precision mode 1):
+ * the f16 plane hi = f16(x) [M,K] followed by the f16 plane lo = f16(x - hi)
+ * [M,K]; the same bytes as f32. tgohip_linear's x_dtype only. */
+#define TGOHIP_F16X2 2
 
 const char* tgohip_last_error(void);
 const char* tgohip_version(void);
@@ -77,10 +81,15 @@ int tgohip_sync(tgohip_ctx* ctx);
  * stream); tgohip_use_own_stream returns to it. */
 int tgohip_set_stream(tgohip_ctx* ctx, void* stream);
 int tgohip_use_own_stream(tgohip_ctx* ctx);
-/* Activation precision of the projections: 0 (default) rounds the activation
- * operand to f16 for the f16 MFMA; 1 carries the f32 activation as an f16
- * high + low pair (two MFMAs), keeping ~22 bits of it -- tgo's f32-activation
- * semantics (nn/blocks.go:13-21) at twice the matrix-core work. */
+/* Arithmetic of the step. 1 is tgo's CPU path (nn/blocks.go:13-21): every
+ * projection multiplies the f32 activation (carried as an f16 high + low pair,
+ * ~22 bits) by the unrounded dequantized weight (carried as an exact f16
+ * high + low pair), f32 accumulate -- three f16 MFMAs per product -- and
+ * attention weights V by the f32 softmax probabilities (hi + lo); logits stay
+ * within 2e-3 of tgo's CPU path through every layer of the 8B and 32B shapes.
+ * 0 rounds activations, weights and probabilities to f16 for one MFMA each:
+ * about 2.4x faster, with an f16 storage error per operand that grows with
+ * depth (about 5e-3 of the row's largest logit after 36 layers). */
 int tgohip_set_precision(tgohip_ctx* ctx, int mode);
 /* Prefix-shared (cascade) attention, the "read a shared page once" design of
  * tgo's prefix cache (internal/prefix block sharing; specs/016-prefix-cache.md).
@@ -220,7 +229,10 @@ int tgohip_weight_synth(tgohip_ctx* ctx, int form, int K, int N, uint64_t seed, 
 int tgohip_weight_free(tgohip_ctx* ctx, int handle);
 
 /* nn.Linear (nn/blocks.go:22-46): y[M,N] = x[M,K] . deq(W)[K,N], f32
- * accumulate. x device [M,K] (x_dtype), y device [M,N] (y_dtype). */
+ * accumulate. x device [M,K] (x_dtype), y device [M,N] (y_dtype). With x_dtype
+ * F32 or F16X2 the product is tgo's arithmetic (the f32 activation times the
+ * unrounded dequantized weight); with F16, the f16 activation times the
+ * dequantized weight rounded to f16. */
 int tgohip_linear(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M, void* y,
                   int y_dtype);
 

@@ -72,12 +72,23 @@ def test_dequant_is_bit_exact(ctx, torch_gpu, form):
         ctx.weight_free(h)
 
 
+def split_pair(x):
+    """An f32 activation as tgo's arithmetic carries it: f16 hi, then f16 lo = f16(x - hi)."""
+    hi = x.astype(np.float16)
+    lo = (x - hi.astype(np.float32)).astype(np.float16)
+    return hi, lo
+
+
 @pytest.mark.parametrize("form", [0, 1, 2, 3])
 @pytest.mark.parametrize("M", [1, 8, 16, 32, 33, 64, 130, 300])
-@pytest.mark.parametrize("xf32", [True, False])
-def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xf32):
+@pytest.mark.parametrize("xk", ["f32", "f16", "x2"])
+def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xk):
+    """xk: f32 activations (split in the kernel), f16, or an activation pair (f16 hi plane
+    then lo plane, the form precision mode 1's producers write; the exact pipelined kernel
+    from 33 rows)."""
     torch = torch_gpu
     import tgo_amd
+    xf32 = xk != "f16"
     rng = np.random.default_rng(100 + form * 7 + M)
     K, N = 512, 256 if form != 2 else 384
     wd, _ = make_weight(form, K, N, rng)
@@ -86,14 +97,19 @@ def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xf32):
     x = rng.standard_normal((M, K)).astype(np.float32)
     h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
     try:
-        if xf32:
+        if xk == "f32":
             dx = torch.from_numpy(x).cuda()
+            xu = x.astype(np.float64)
+        elif xk == "x2":
+            hi, lo = split_pair(x)
+            dx = torch.from_numpy(np.concatenate([hi.ravel(), lo.ravel()])).cuda()
             xu = x.astype(np.float64)
         else:
             dx = torch.from_numpy(x.astype(np.float16)).cuda()
             xu = x.astype(np.float16).astype(np.float64)
         y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-        ctx.linear(h, dx, M, y, x_dtype=tgo_amd.F32 if xf32 else tgo_amd.F16)
+        ctx.linear(h, dx, M, y, x_dtype={"f32": tgo_amd.F32, "f16": tgo_amd.F16,
+                                         "x2": tgo_amd.F16X2}[xk])
         torch.cuda.synchronize()
         got = y.cpu().numpy().astype(np.float64)
     finally:

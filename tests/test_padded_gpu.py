@@ -202,13 +202,14 @@ def test_padding_row_inside_the_pool_writes_its_kv(torch_gpu):
 
 @pytest.mark.timeout(900)
 def test_c4_step_bucketed_to_2048_rows_matches_the_cpu_path(torch_gpu):
-    """bench.py's C4 step (130 members, 1152 rows, 8B widths, int4, two layers deep, the
-    bench's f16-activation mode) padded to the 2048-row rung of tgo's bucket ladder."""
+    """bench.py's C4 step (130 members, 1152 rows, 8B widths, int4, two layers deep, tgo's
+    f32 arithmetic: precision mode 1) padded to the 2048-row rung of tgo's bucket ladder."""
     from test_config_gpu import copy_pool, cpu_model, open_ctx
     torch = torch_gpu
     cfg, form, pool = bench.C4, tgo_amd.FORM_I4_SYM, bench.POOL
     layers = 2
     ctx = open_ctx(cfg, form, pool, bench.SEED)
+    ctx.set_precision(1)
     cpu = None
     try:
         wl = bench.Workload(tgo_amd, ctx, bench.SEED)

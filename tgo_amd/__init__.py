@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtgohip.so")
 
 FORM_F16, FORM_I8, FORM_I4_TGO, FORM_I4_SYM = 0, 1, 2, 3
-F32, F16 = 0, 1
+F32, F16, F16X2 = 0, 1, 2
 PROF_ATTN, PROF_QKV, PROF_O, PROF_GATEUP, PROF_DOWN, PROF_LMHEAD = range(6)
 PROF_NAMES = ("attention", "qkv", "o", "gateup", "down", "lm_head")
 

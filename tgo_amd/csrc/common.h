@@ -84,7 +84,19 @@ struct AttnPlan {
 
 
 // ---- GEMM (kernels/gemm.hip) --------------------------------------------
-enum { EPI_F32 = 0, EPI_F16 = 1, EPI_RESID = 2, EPI_SWIGLU_F16 = 3, EPI_SWIGLU_F32 = 4 };
+// EPI_SWIGLU_X2 stores the SwiGLU output as an activation pair (below).
+enum { EPI_F32 = 0, EPI_F16 = 1, EPI_RESID = 2, EPI_SWIGLU_F16 = 3, EPI_SWIGLU_F32 = 4,
+       EPI_SWIGLU_X2 = 5 };
+// How an activation [M][K] is stored for a projection:
+//   XK_F16  f16, rounded once (the fast f16 path, precision mode 0);
+//   XK_F32  f32 (tgo's arithmetic; split into f16 hi + lo inside the kernel);
+//   XK_X2   tgo's f32 activation already split by its producer: the f16 hi
+//           plane [M][K] followed by the lo plane [M][K] (lo = f16(x - hi)),
+//           so hi + lo carries ~22 bits of x. Same bytes as f32.
+enum { XK_F16 = 0, XK_F32 = 1, XK_X2 = 2 };
+// Output forms of the per-row producers (rmsnorm, attention): 0 f32, 1 f16,
+// 2 the hi/lo pair of XK_X2 (lo plane `rows * width` elements after hi).
+enum { OUT_F32 = 0, OUT_F16 = 1, OUT_X2 = 2 };
 
 // A weight in the fragment-major device layout (see kernels/gemm.hip).
 struct PackedWeight {
@@ -101,15 +113,15 @@ size_t packed_scale_halves(int form, int K, int N);
 int repack_enqueue(int form, const void* plane, const uint16_t* scales, const uint16_t* zeros,
                    int K, int N, PackedWeight& w, int nb_stride, int nb_off, hipStream_t st);
 int dequant_enqueue(const PackedWeight& w, void* out, bool f16out, hipStream_t st);
-// Split-K workspace of a call: x_f32 < 0 bounds every activation type and
-// epilogue; 0/1 gives exactly what an f32/f16-epilogue call over f16/f32
-// activations uses.
-size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int x_f32 = -1);
+// Split-K workspace of a call: xk < 0 bounds every activation type and
+// epilogue; an XK_* value gives exactly what an f32/f16-epilogue call over
+// that activation type uses.
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int xk = -1);
 // With defer != nullptr a split-K launch leaves its partial planes in the
 // workspace ([splits][M][N] f32) and sets *defer = splits instead of running
 // the reduction; the caller folds them into the consumer (rmsnorm,
 // qk_rope_kv). *defer = 0 when the epilogue ran as usual.
-int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
+int gemm_enqueue(const PackedWeight& w, const void* x, int xk, int M, void* y, int epi,
                  float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer = nullptr);
 
 // ---- attention (kernels/attention.hip) -----------------------------------
@@ -127,8 +139,9 @@ struct AttnDevPlan {
 int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
                     const uint32_t* pages, int max_pages, int block, int capacity, int H,
                     int Hkv, AttnPlan& plan, int cascade_min = 0);
+// out_form: OUT_F32, OUT_F16 or OUT_X2 (lo plane T * H * 128 elements after hi).
 int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int q_f16,
-                 const void* k, const void* v, void* out, int out_f16, int T, int H, int Hkv,
+                 const void* k, const void* v, void* out, int out_form, int T, int H, int Hkv,
                  int max_pages, int block, float scale, hipStream_t stream);
 
 // ---- per-row kernels (kernels/elementwise.hip) ---------------------------
@@ -162,8 +175,9 @@ struct QKRopeArgs {
 // feed[b] (the previous step's argmax, left on the device).
 void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,
                   int d, float* h, hipStream_t st, const int32_t* feed = nullptr);
+// out_form: OUT_F32, OUT_F16 or OUT_X2 (lo plane nrows * w elements after hi).
 void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
-                    float eps, void* out, int out_f16, hipStream_t st, const float* part = nullptr,
+                    float eps, void* out, int out_form, hipStream_t st, const float* part = nullptr,
                     int nsplit = 0, size_t plane = 0);
 void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st);
 // posq/posk/slots derived on the device from the members (NewBatchStep's

@@ -55,7 +55,8 @@ struct AttnArgs {
   const uint32_t* lengths;
   const uint32_t* extents;
   const uint32_t* pages;
-  int q_f16, out_f16;
+  int q_f16, out_f16;  // out_f16: OUT_F32, OUT_F16 or OUT_X2
+  size_t out_lo;       // OUT_X2: elements from the hi plane to the lo plane (T * H * 128)
   int max_pages, block, H, Hkv, G;
   float qscale;  // scale * log2(e)
 };
@@ -71,12 +72,22 @@ __device__ __forceinline__ float wave_sum16x(float v) {
   return v;
 }
 
-__device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const float* v) {
+// Eight output values as f32, f16, or (OUT_X2) the f16 hi plane plus the lo
+// plane f16(v - hi) lo elements further on: the activation pair the exact
+// projections read.
+__device__ __forceinline__ void store_out8(void* out, int f16, size_t off, const float* v,
+                                           size_t lo = 0) {
   if (f16) {
     half8_t h;
 #pragma unroll
     for (int j = 0; j < 8; j++) h[j] = (half_t)v[j];
     *(half8_t*)((half_t*)out + off) = h;
+    if (f16 == OUT_X2) {
+      half8_t l;
+#pragma unroll
+      for (int j = 0; j < 8; j++) l[j] = (half_t)(v[j] - (float)h[j]);
+      *(half8_t*)((half_t*)out + lo + off) = l;
+    }
   } else {
     float4_t a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
     *(float4_t*)((float*)out + off) = a;
@@ -484,7 +495,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, const AttnItem& i
 #pragma unroll
       for (int j = 0; j < 8; j++) acc[j] *= inv;
       const int tk = it.tok0 + row / G, hd = c.kvh * G + row % G;
-      store_out8(a.out, a.out_f16, ((size_t)(c.cu + tk) * a.H + hd) * kHeadDim + d0, acc);
+      store_out8(a.out, a.out_f16, ((size_t)(c.cu + tk) * a.H + hd) * kHeadDim + d0, acc, a.out_lo);
     } else {
       float* po = a.part_o + ((size_t)it.part * kAttnRowsP + row) * 128 + d0;
 #pragma unroll
@@ -644,6 +655,12 @@ __device__ __forceinline__ void attn_prefill(const AttnArgs& a, const AttnItem& 
 #pragma unroll
           for (int q = 0; q < 4; q++) hv[q] = (half_t)(o[db][4 * g + q] * inv);
           *(half4_t*)((half_t*)a.out + off) = hv;
+          if (a.out_f16 == OUT_X2) {
+            half4_t lv;
+#pragma unroll
+            for (int q = 0; q < 4; q++) lv[q] = (half_t)(o[db][4 * g + q] * inv - (float)hv[q]);
+            *(half4_t*)((half_t*)a.out + a.out_lo + off) = lv;
+          }
         } else {
           const float4_t fv = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
                                o[db][4 * g + 3] * inv};
@@ -755,16 +772,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] *= inv;
     const int tok = cb.tok0 + row / G, head = cb.kvh * G + row % G;
-    store_out8(a.out, a.out_f16, ((size_t)(a.cu[cb.seq] + tok) * a.H + head) * kHeadDim + d0, acc);
+    store_out8(a.out, a.out_f16, ((size_t)(a.cu[cb.seq] + tok) * a.H + head) * kHeadDim + d0, acc,
+               a.out_lo);
   }
 }
 
 // Zeroes rows [r0, r1) of a [T, width] activation: the inert pad rows.
-__global__ void zero_rows_kernel(void* out, int f16, size_t start, size_t count) {
+__global__ void zero_rows_kernel(void* out, int f16, size_t start, size_t count, size_t lo) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= count) return;
   if (f16) ((half_t*)out)[start + i] = (half_t)0.f;
   else ((float*)out)[start + i] = 0.f;
+  if (f16 == OUT_X2) ((half_t*)out)[lo + start + i] = (half_t)0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -1072,7 +1091,7 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
 }
 
 int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int q_f16,
-                 const void* k, const void* v, void* out, int out_f16, int T, int H, int Hkv,
+                 const void* k, const void* v, void* out, int out_form, int T, int H, int Hkv,
                  int max_pages, int block, float scale, hipStream_t stream) {
   AttnArgs a;
   a.q = q;
@@ -1089,7 +1108,8 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
   a.extents = dp.extents;
   a.pages = dp.pages;
   a.q_f16 = q_f16;
-  a.out_f16 = out_f16;
+  a.out_f16 = out_form;
+  a.out_lo = (size_t)T * H * kHeadDim;
   a.max_pages = max_pages;
   a.block = block;
   a.H = H;
@@ -1121,7 +1141,7 @@ int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int
     const size_t start = (size_t)plan.claimed * H * kHeadDim;
     const size_t count = (size_t)(T - plan.claimed) * H * kHeadDim;
     hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
-                       stream, out, out_f16, start, count);
+                       stream, out, out_form, start, count, a.out_lo);
   }
   TGOHIP_HIP(hipGetLastError());
   return 0;

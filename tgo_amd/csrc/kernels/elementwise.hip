@@ -102,10 +102,12 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // R > 0: every thread owns at most R float4s of the row (w <= 4 R blockDim.x)
 // and keeps them in registers between the sum of squares and the scaling;
 // R = 0: any width, the second pass reloads the row.
+// out_form OUT_X2: the f32 result as its f16 hi plane [nrows][w] and lo plane
+// (f16(x - hi)) right after it, the activation pair the exact projections read.
 template <int R>
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t* rows,
                                                        const float* g, int w, float eps,
-                                                       void* out, int out_f16, const float* part,
+                                                       void* out, int out_form, const float* part,
                                                        int nsplit, size_t plane) {
   __shared__ float red[16];
   const int r = blockIdx.x;
@@ -116,11 +118,17 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* x, const uint32_t*
     float4_t o;
 #pragma unroll
     for (int j = 0; j < 4; j++) o[j] = v[j] * sc * gg[j];
-    if (out_f16) {
+    if (out_form == OUT_F32) {
+      *(float4_t*)((float*)out + (size_t)r * w + i) = o;
+    } else {
       half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
       *(half4_t*)((half_t*)out + (size_t)r * w + i) = hv;
-    } else {
-      *(float4_t*)((float*)out + (size_t)r * w + i) = o;
+      if (out_form == OUT_X2) {
+        half4_t lv;
+#pragma unroll
+        for (int j = 0; j < 4; j++) lv[j] = (half_t)(o[j] - (float)hv[j]);
+        *(half4_t*)((half_t*)out + (size_t)gridDim.x * w + (size_t)r * w + i) = lv;
+      }
     }
   };
   float ss = 0.f;
@@ -536,13 +544,13 @@ void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t*
   hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, st, ids, table, scales, form, d, h, feed);
 }
 void launch_rmsnorm(float* x, const uint32_t* rows, int nrows, const float* g, int w,
-                    float eps, void* out, int out_f16, hipStream_t st, const float* part,
+                    float eps, void* out, int out_form, hipStream_t st, const float* part,
                     int nsplit, size_t plane) {
   const int threads = std::min(1024, std::max(64, (w / 4 + 63) / 64 * 64));
   const int per = (w + 4 * threads - 1) / (4 * threads);  // float4s per thread
 #define RMSNORM_LAUNCH(R)                                                                      \
   hipLaunchKernelGGL(rmsnorm_kernel<R>, dim3(nrows), dim3(threads), 0, st, x, rows, g, w, eps, \
-                     out, out_f16, part, nsplit, plane)
+                     out, out_form, part, nsplit, plane)
   if (per <= 1) RMSNORM_LAUNCH(1);
   else if (per == 2) RMSNORM_LAUNCH(2);
   else if (per <= 4) RMSNORM_LAUNCH(4);

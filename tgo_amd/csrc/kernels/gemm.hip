@@ -36,7 +36,8 @@
 namespace tgohip {
 
 struct GemmArgs {
-  const void* x;        // [M,K] f16 or f32
+  const void* x;        // [M,K] f16 or f32 (or the hi plane of an XK_X2 pair)
+  const void* xlo;      // XK_X2: the lo plane [M,K] f16; null otherwise
   const void* wp;       // packed payload
   const half_t* ws;     // packed scales (form dependent)
   const half_t* wz;     // packed zero+1024 (I4_TGO only)
@@ -306,6 +307,20 @@ __device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_r
 // conflict-free.
 __device__ __forceinline__ int a_slot(int row, int kc) { return row * 8 + (kc ^ ((row >> 1) & 7)); }
 
+// One SwiGLU output at element o of [M, N/2]: f16, f32, or the f16 hi plane
+// and the lo plane (f16(v - hi)) M*N/2 elements after it (the activation pair
+// the exact down projection reads).
+template <int EPI>
+__device__ __forceinline__ void store_swiglu(const GemmArgs& g, size_t o, float v) {
+  if (EPI == EPI_SWIGLU_F32) {
+    ((float*)g.y)[o] = v;
+  } else {
+    const half_t h = (half_t)v;
+    ((half_t*)g.y)[o] = h;
+    if (EPI == EPI_SWIGLU_X2) ((half_t*)g.y)[(size_t)g.M * (g.N / 2) + o] = (half_t)(v - (float)h);
+  }
+}
+
 // Epilogue shared by the GEMM kernels. Lane holds D[8*(r/4) + 4*h + (r%4)][c32]
 // of each 32x32 block; a split-K launch writes f32 partials for its split.
 template <int EPI, int MB>
@@ -323,13 +338,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const float16_t
 #pragma unroll
         for (int b = 0; b < 2; b++)
           if (nbv[b]) dst[(nbw0 + b) * 32 + c32] = acc[mb][b][r];
-      } else if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+      } else if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32 || EPI == EPI_SWIGLU_X2) {
         if (nbv[1]) {
           const float v = silu_f(acc[mb][0][r]) * acc[mb][1][r];
           const int col = (nbw0 >> 1) * 32 + c32;
           const size_t o = (size_t)row * (g.N / 2) + col;
-          if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[o] = (half_t)v;
-          else ((float*)g.y)[o] = v;
+          store_swiglu<EPI>(g, o, v);
         }
       } else {
 #pragma unroll
@@ -386,7 +400,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       const int gm = m0 + row;
       if (gm < g.M) {
         const size_t off = (size_t)gm * g.K + ks * 64 + kc * 8;
-        if (ASPLIT) {
+        if (ASPLIT && g.xlo) {
+          // an XK_X2 pair: hi and lo as their producer split them
+          areg[i][0] = *(const uint4*)((const half_t*)g.x + off);
+          areg[i][APLANES - 1] = *(const uint4*)((const half_t*)g.xlo + off);
+        } else if (ASPLIT) {
           const float4_t u = *(const float4_t*)((const float*)g.x + off);
           const float4_t w = *(const float4_t*)((const float*)g.x + off + 4);
           const float v[8] = {u[0], u[1], u[2], u[3], w[0], w[1], w[2], w[3]};
@@ -542,24 +560,62 @@ __device__ __forceinline__ half8_t pipe_bfrag(const PipeB<TGOHIP_FORM_I8>& r, in
   return deq_i8((j & 1) ? q.z : q.x, (j & 1) ? q.w : q.y, s8);
 }
 
+// Substep j's B fragment as the exact hi + lo pair (bfrag_split).
+__device__ __forceinline__ void pipe_bfrag_x(const PipeB<TGOHIP_FORM_I4_SYM>& r, int j,
+                                             const half_t*, int, int, half8_t& hi, half8_t& lo) {
+  BRaw<TGOHIP_FORM_I4_SYM> x;
+  x.p = r.p;
+  x.s = r.s;
+  bfrag_split(x, j, hi, lo);
+}
+__device__ __forceinline__ void pipe_bfrag_x(const PipeB<TGOHIP_FORM_I4_TGO>& r, int j,
+                                             const half_t* sz, int b, int h, half8_t& hi,
+                                             half8_t& lo) {
+  BRaw<TGOHIP_FORM_I4_TGO> x;
+  x.p = r.p;
+  U16B sv, zv;
+  sv.h = *(const half8_t*)(sz + b * 64 + (2 * j + h) * 8);
+  zv.h = *(const half8_t*)(sz + 128 + b * 64 + (2 * j + h) * 8);
+  x.s[j] = sv.u;
+  x.z[j] = zv.u;
+  bfrag_split(x, j, hi, lo);
+}
+__device__ __forceinline__ void pipe_bfrag_x(const PipeB<TGOHIP_FORM_I8>& r, int j,
+                                             const half_t* sz, int b, int h, half8_t& hi,
+                                             half8_t& lo) {
+  BRaw<TGOHIP_FORM_I8> x;
+  x.p[0] = r.p[0];
+  x.p[1] = r.p[1];
+  U16B sv;
+  sv.h = *(const half8_t*)(sz + b * 64 + (2 * j + h) * 8);
+  x.s[j] = sv.u;
+  bfrag_split(x, j, hi, lo);
+}
+
 // NW waves (4 or 8) side by side in N: a workgroup owns MW rows x 64*NW
 // columns. With KQ = 2 the workgroup holds two such groups of NW waves, each
 // over one half of the workgroup's k-steps with its own A ring, and group 1
 // hands its sums to group 0 through LDS at the end (acc0 + acc1, a fixed
 // order): two waves per SIMD where the tiles alone would give one.
-template <int FORM, int EPI, int MW, int NW, int KQ = 1>
+// EX (tgo's f32 arithmetic, XK_X2 activations): the A tile is the activation
+// pair, hi and lo planes DMA'd side by side into each stage, and the weights
+// the exact hi + lo pair (pipe_bfrag_x): three MFMAs per product (hi.hi,
+// lo.hi, hi.lo), the f32 activation times the unrounded dequantized weight.
+template <int FORM, int EPI, int MW, int NW, int KQ = 1, bool EX = false>
 __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_kernel(
     GemmArgs g, int tiles_n, int tiles, int colmajor, int xsplit) {
   constexpr int MB = MW / 32;
-  constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step
+  constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step and plane
+  constexpr int AP = EX ? 2 : 1;      // activation planes per stage
   static_assert(KQ == 1 || (KQ == 2 && NW * MW * 256 <= 4 * 2 * MW * 128),
                 "group 1's sums fit in the A ring");
   // Four LDS stages, separate arrays so the compiler can tell a DMA into one
-  // stage from reads of another; group q's tile at q * MW * 64 of each.
-  __shared__ __attribute__((aligned(16))) half_t As0[KQ * MW * 64];
-  __shared__ __attribute__((aligned(16))) half_t As1[KQ * MW * 64];
-  __shared__ __attribute__((aligned(16))) half_t As2[KQ * MW * 64];
-  __shared__ __attribute__((aligned(16))) half_t As3[KQ * MW * 64];
+  // stage from reads of another; group q's tile at q * AP * MW * 64 of each
+  // (with EX its lo plane MW * 64 halves after its hi plane).
+  __shared__ __attribute__((aligned(16))) half_t As0[KQ * AP * MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As1[KQ * AP * MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As2[KQ * AP * MW * 64];
+  __shared__ __attribute__((aligned(16))) half_t As3[KQ * AP * MW * 64];
   half_t* const As[4] = {As0, As1, As2, As3};
   // Per-stage scales and zeros of the waves' column blocks (int8, tgo int4).
   constexpr bool LS = pipe_lds_scales<FORM>();
@@ -614,7 +670,7 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
   const int nkw = min(KS, split * g.ksteps_per_split + g.ksteps_per_split) - split * g.ksteps_per_split;
   const int nk = nkw / KQ;
   const int ks0 = split * g.ksteps_per_split + kq * nk;
-  const int aq = kq * MW * 64, sq = kq * SZN;  // the group's offsets in each A and scale stage
+  const int aq = kq * AP * MW * 64, sq = kq * SZN;  // the group's offsets in each A and scale stage
   const bool nbv[2] = {nbw0 < NBT, nbw0 + 1 < NBT};
   // Out-of-range column blocks load a valid block (results are not stored).
   const int nbl[2] = {min(nbw0, NBT - 1), min(nbw0 + 1, NBT - 1)};
@@ -631,6 +687,7 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
     doff[i] = ((uint32_t)min(m0 + row, g.M - 1) * (uint32_t)g.K + (uint32_t)(kc * 8)) * 2u;
   }
   const char* xa = (const char*)g.x;
+  const char* xl = (const char*)g.xlo;  // EX: the lo plane (same offsets)
   PipeB<FORM> bq[4][2];  // B(k) in slot k % 4, all four live
   // A wave's scales (lanes 0-15: blocks nbl[0], nbl[1]) and zeros (lanes
   // 16-31) of one k-step are 128-byte runs of the packed arrays.
@@ -644,6 +701,12 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
         __builtin_amdgcn_global_load_lds(                                              \
             (const __attribute__((address_space(1))) void*)(xa + (size_t)(ks) * 128 + doff[i]), \
             (__attribute__((address_space(3))) void*)(As[stage] + aq + (NW * i + wave) * 512), 16, 0, 0); \
+    if (EX)                                                                            \
+      _Pragma("unroll") for (int i = 0; i < ACH; i++)                                  \
+          __builtin_amdgcn_global_load_lds(                                            \
+              (const __attribute__((address_space(1))) void*)(xl + (size_t)(ks) * 128 + doff[i]), \
+              (__attribute__((address_space(3))) void*)(As[stage] + aq + MW * 64 + (NW * i + wave) * 512), \
+              16, 0, 0);                                                               \
     if (LS && szlane)                                                                  \
       __builtin_amdgcn_global_load_lds(                                                \
           (const __attribute__((address_space(1))) void*)(szsrc + (size_t)(ks) * 128), \
@@ -672,7 +735,25 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
   // barrier reuses. The barrier carries no memory fence: a fence would wait
   // for every DMA in flight.
   auto kpos = [&](int k) { return ks0 + min(k, nk - 1); };
-  half8_t afc[MB], bfc[2];
+  // Substep fragments: A rows (hi; with EX also lo) and B blocks (hi; with EX
+  // the exact weight's lo part too).
+  half8_t afc[MB], bfc[2], afcl[MB], bfcl[2];
+  constexpr int LOP = MW * 8;  // half8s from a stage's hi plane to its lo plane
+  auto read_a = [&](const half8_t* A, int kc, half8_t (&ah)[MB], half8_t (&al)[MB]) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      ah[mb] = A[a_slot(mb * 32 + c32, kc)];
+      if (EX) al[mb] = A[LOP + a_slot(mb * 32 + c32, kc)];
+    }
+  };
+  auto read_b = [&](const PipeB<FORM>(&bb)[2], int j, const half_t* sz, half8_t (&bh)[2],
+                    half8_t (&bl)[2]) {
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      if constexpr (EX) pipe_bfrag_x(bb[b], j, sz, b, h, bh[b], bl[b]);
+      else bh[b] = pipe_bfrag(bb[b], j, sz, b, h);
+    }
+  };
   if (nk > 0) {  // nk is then a multiple of 4 (the host guarantees it)
 #pragma unroll
     for (int b = 0; b < 2; b++) load_pipeb(g, nbl[b], kpos(0), lane, bq[0][b]);
@@ -687,11 +768,8 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const half8_t* A = (const half8_t*)(As[0] + aq);
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) afc[mb] = A[a_slot(mb * 32 + c32, h)];
-#pragma unroll
-    for (int b = 0; b < 2; b++) bfc[b] = pipe_bfrag(bq[0][b], 0, Sz[0] + sq + wave * 256, b, h);
+    read_a((const half8_t*)(As[0] + aq), h, afc, afcl);
+    read_b(bq[0], 0, Sz[0] + sq + wave * 256, bfc, bfcl);
   }
   for (int kk = 0; kk < nk; kk += 4) {
 #pragma unroll
@@ -712,40 +790,69 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
       // fed.
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        half8_t afn[MB], bfn[2];
+        half8_t afn[MB], bfn[2], afnl[MB], bfnl[2];
         if (j < 3) {
-#pragma unroll
-          for (int mb = 0; mb < MB; mb++) afn[mb] = A[a_slot(mb * 32 + c32, 2 * (j + 1) + h)];
-#pragma unroll
-          for (int b = 0; b < 2; b++) bfn[b] = pipe_bfrag(bq[u][b], j + 1, Sz[u] + sq + wave * 256, b, h);
+          read_a(A, 2 * (j + 1) + h, afn, afnl);
+          read_b(bq[u], j + 1, Sz[u] + sq + wave * 256, bfn, bfnl);
         } else {
-#pragma unroll
-          for (int mb = 0; mb < MB; mb++) afn[mb] = An[a_slot(mb * 32 + c32, h)];
-#pragma unroll
-          for (int b = 0; b < 2; b++)
-            bfn[b] = pipe_bfrag(bq[(u + 1) % 4][b], 0, Sz[(u + 1) % 4] + sq + wave * 256, b, h);
+          read_a(An, h, afn, afnl);
+          read_b(bq[(u + 1) % 4], 0, Sz[(u + 1) % 4] + sq + wave * 256, bfn, bfnl);
         }
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
 #pragma unroll
           for (int b = 0; b < 2; b++)
             acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
+        if constexpr (EX) {
+          // the two correction products, each pass over every block, so no
+          // MFMA waits on the one just issued into the same accumulator
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afcl[mb], bfc[b], acc[mb][b], 0, 0, 0);
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfcl[b], acc[mb][b], 0, 0, 0);
+        }
+        if constexpr (EX) {
+          // 12 MFMAs (64-row tiles), 4 LDS reads, the B pairs' ~34 VALU
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+          }
         }
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) afc[mb] = afn[mb];
+        for (int mb = 0; mb < MB; mb++) {
+          afc[mb] = afn[mb];
+          afcl[mb] = afnl[mb];
+        }
 #pragma unroll
-        for (int b = 0; b < 2; b++) bfc[b] = bfn[b];
+        for (int b = 0; b < 2; b++) {
+          bfc[b] = bfn[b];
+          bfcl[b] = bfnl[b];
+        }
         if (j == 1) {
           __builtin_amdgcn_sched_barrier(0);
           // vmcnt(2 * B loads + A DMA + scale DMA), expcnt untouched, lgkmcnt(0)
-          __builtin_amdgcn_s_waitcnt((2 * pipe_b_loads<FORM>() + ACH + (LS ? 1 : 0)) | (7 << 4));
+          static_assert(2 * pipe_b_loads<FORM>() + AP * ACH + 1 < 16, "vmcnt fits 4 bits");
+          __builtin_amdgcn_s_waitcnt((2 * pipe_b_loads<FORM>() + AP * ACH + (LS ? 1 : 0)) | (7 << 4));
           asm volatile("" ::: "memory");
           __builtin_amdgcn_s_barrier();
           asm volatile("" ::: "memory");
@@ -824,18 +931,17 @@ __device__ __forceinline__ float sum_split_values(const float* p, int splits, si
 // Sums split-K partials in split order and applies the epilogue.
 template <int EPI>
 __global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
-  const int outN = (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) ? g.N / 2 : g.N;
+  constexpr bool SW = EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32 || EPI == EPI_SWIGLU_X2;
+  const int outN = SW ? g.N / 2 : g.N;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)g.M * outN) return;
   const int row = (int)(i / outN), col = (int)(i % outN);
   const size_t plane = g.pstride;
-  if (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+  if (SW) {
     const int gc = (col / 32) * 64 + (col % 32), uc = gc + 32;
     const float ga = sum_split_values(g.part + (size_t)row * g.N + gc, splits, plane);
     const float ua = sum_split_values(g.part + (size_t)row * g.N + uc, splits, plane);
-    const float v = silu_f(ga) * ua;
-    if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[i] = (half_t)v;
-    else ((float*)g.y)[i] = v;
+    store_swiglu<EPI>(g, i, silu_f(ga) * ua);
   } else {
     const float a = sum_split_values(g.part + i, splits, plane);
     if (EPI == EPI_F32) ((float*)g.y)[i] = a;
@@ -1072,12 +1178,10 @@ __host__ __device__ constexpr int gemv_stage_stride(int K) { return K + 8; }
 template <int EPI, int CB>
 __device__ __forceinline__ void gemv_store(const GemmArgs& g, int nbw0, const bool (&nbv)[CB], int row,
                                            int col, const float (&v)[CB]) {
-  if constexpr (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32) {
+  if constexpr (EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32 || EPI == EPI_SWIGLU_X2) {
     if (!nbv[CB - 1]) return;
-    const float o = silu_f(v[0]) * v[CB - 1];
     const size_t off = (size_t)row * (g.N / 2) + (nbw0 >> 1) * 32 + col;
-    if (EPI == EPI_SWIGLU_F16) ((half_t*)g.y)[off] = (half_t)o;
-    else ((float*)g.y)[off] = o;
+    store_swiglu<EPI>(g, off, silu_f(v[0]) * v[CB - 1]);
   } else {
 #pragma unroll
     for (int b = 0; b < CB; b++) {
@@ -1314,8 +1418,8 @@ static void launch_gemv_form(const GemmArgs& g, int epi, const GemvShape& sh, hi
 
 // The small-M kernels serve f16 activations up to 32 rows when K's k-steps
 // divide into whole-depth shares.
-static bool use_gemv(const PackedWeight& w, bool x_f32, int M, int ncu) {
-  return !x_f32 && M <= 32 && gemv_shape(w, EPI_F32, M, ncu).w > 0;
+static bool use_gemv(const PackedWeight& w, int xk, int M, int ncu) {
+  return xk == XK_F16 && M <= 32 && gemv_shape(w, EPI_F32, M, ncu).w > 0;
 }
 
 // Split-K factor: enough workgroups to cover the chip twice, while each split
@@ -1337,6 +1441,9 @@ static void launch_form(const GemmArgs& g, int epi, dim3 grid, hipStream_t st) {
     case EPI_RESID: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_RESID>), grid, blk, 0, st, g); break;
     case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_SWIGLU_F16>), grid, blk, 0, st, g); break;
     case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_SWIGLU_F32>), grid, blk, 0, st, g); break;
+    case EPI_SWIGLU_X2:
+      if constexpr (ASPLIT) hipLaunchKernelGGL((gemm_kernel<FORM, MW, ASPLIT, EPI_SWIGLU_X2>), grid, blk, 0, st, g);
+      break;
   }
 }
 
@@ -1351,7 +1458,7 @@ static void launch_mw(int form, const GemmArgs& g, int epi, dim3 grid, hipStream
 }
 
 static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st) {
-  const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) ? g.N / 2 : g.N;
+  const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) ? g.N / 2 : g.N;
   const size_t total = (size_t)g.M * outN;
   const dim3 rg((unsigned)((total + 255) / 256)), rb(256);
   switch (epi) {
@@ -1360,6 +1467,7 @@ static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st
     case EPI_RESID: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RESID>, rg, rb, 0, st, g, splits); break;
     case EPI_SWIGLU_F16: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F16>, rg, rb, 0, st, g, splits); break;
     case EPI_SWIGLU_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_F32>, rg, rb, 0, st, g, splits); break;
+    case EPI_SWIGLU_X2: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_SWIGLU_X2>, rg, rb, 0, st, g, splits); break;
   }
 }
 
@@ -1403,9 +1511,11 @@ static int choose_pipe_splits(int tiles, int KS, int slots) {
 // A SwiGLU epilogue needs whole sums, so a split gate/up goes through a
 // separate reduction; with half the CUs covered by tiles it runs unsplit
 // (at 128 rows: 45.6 us unsplit against 45.4 us plus a 7 us reduction).
+// The exact (EX) kernel runs 64-row tiles 4 waves wide at every M: its A ring
+// holds two planes, and at 128 rows its fragments would not fit the registers.
 static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, int& tiles_n,
-                       int& tiles, int& splits, int epi = EPI_F32) {
-  mw = M <= 384 ? 64 : 128;
+                       int& tiles, int& splits, int epi = EPI_F32, bool ex = false) {
+  mw = (M <= 384 || ex) ? 64 : 128;
   const int nb = w.N / 32, rows = (M + mw - 1) / mw;
   nw = 4;
   if (mw == 128) {
@@ -1419,27 +1529,34 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
   tiles_n = (nb + 2 * nw - 1) / (2 * nw);
   tiles = tiles_n * rows;
   splits = choose_pipe_splits(tiles, w.K / 64, ncu * (8 / nw));
-  if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) && tiles >= ncu / 2) splits = 1;
+  if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) && tiles >= ncu / 2)
+    splits = 1;
 }
 
 
-template <int FORM, int MW, int NW, int KQ = 1>
+template <int FORM, int MW, int NW, int KQ = 1, bool EX = false>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
                              int cm, int xs, hipStream_t st) {
   const dim3 blk(64 * NW * KQ);
+#define PIPE_LAUNCH(E) \
+  hipLaunchKernelGGL((gemm_pipe_kernel<FORM, E, MW, NW, KQ, EX>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs)
   switch (epi) {
-    case EPI_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F32, MW, NW, KQ>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
-    case EPI_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_F16, MW, NW, KQ>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_RESID, MW, NW, KQ>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
-    case EPI_SWIGLU_F16: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F16, MW, NW, KQ>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
-    case EPI_SWIGLU_F32: hipLaunchKernelGGL((gemm_pipe_kernel<FORM, EPI_SWIGLU_F32, MW, NW, KQ>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs); break;
+    case EPI_F32: PIPE_LAUNCH(EPI_F32); break;
+    case EPI_F16: PIPE_LAUNCH(EPI_F16); break;
+    case EPI_RESID: PIPE_LAUNCH(EPI_RESID); break;
+    case EPI_SWIGLU_F16: if constexpr (!EX) PIPE_LAUNCH(EPI_SWIGLU_F16); break;
+    case EPI_SWIGLU_F32: if constexpr (!EX) PIPE_LAUNCH(EPI_SWIGLU_F32); break;
+    case EPI_SWIGLU_X2: if constexpr (EX) PIPE_LAUNCH(EPI_SWIGLU_X2); break;
   }
+#undef PIPE_LAUNCH
 }
 
 template <int FORM>
 static void launch_pipe_shape(const GemmArgs& g, int epi, dim3 grid, int mw, int nw, int kq,
-                              int tiles_n, int tiles, int cm, int xs, hipStream_t st) {
-  if (mw == 64 && kq == 2) launch_pipe_form<FORM, 64, 4, 2>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+                              int tiles_n, int tiles, int cm, int xs, bool ex, hipStream_t st) {
+  if (ex && kq == 2) launch_pipe_form<FORM, 64, 4, 2, true>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+  else if (ex) launch_pipe_form<FORM, 64, 4, 1, true>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+  else if (mw == 64 && kq == 2) launch_pipe_form<FORM, 64, 4, 2>(g, epi, grid, tiles_n, tiles, cm, xs, st);
   else if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
   else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, cm, xs, st);
   else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
@@ -1459,9 +1576,9 @@ static bool pipe_kq_enabled() {
 struct PipeLaunch {
   int mw, nw, tiles_n, tiles, splits, kq, ksteps_per_split;
 };
-static PipeLaunch pipe_launch(const PackedWeight& w, int M, int ncu, int epi) {
+static PipeLaunch pipe_launch(const PackedWeight& w, int M, int ncu, int epi, bool ex) {
   PipeLaunch p;
-  pipe_shape(w, M, ncu, p.mw, p.nw, p.tiles_n, p.tiles, p.splits, epi);
+  pipe_shape(w, M, ncu, p.mw, p.nw, p.tiles_n, p.tiles, p.splits, epi, ex);
   const int KS = w.K / 64;
   // Two k groups per workgroup (KQ = 2) where unsplit 64-row tiles would put
   // at most one wave on each SIMD (at most one workgroup per CU): the SwiGLU
@@ -1475,13 +1592,17 @@ static PipeLaunch pipe_launch(const PackedWeight& w, int M, int ncu, int epi) {
   return p;
 }
 
-static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* y, int epi,
-                             float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
-  const PipeLaunch pl = pipe_launch(w, M, ncu, epi);
+// xlo: the lo plane of an XK_X2 activation (the exact kernel), or null.
+static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, const void* xlo, int M, void* y,
+                             int epi, float* workspace, size_t ws_bytes, int ncu, hipStream_t st,
+                             int* defer) {
+  const bool ex = xlo != nullptr;
+  const PipeLaunch pl = pipe_launch(w, M, ncu, epi, ex);
   const int mw = pl.mw, nw = pl.nw, tiles_n = pl.tiles_n, tiles = pl.tiles, kq = pl.kq;
   int splits = pl.splits;
   GemmArgs g{};
   g.x = x;
+  g.xlo = xlo;
   g.wp = w.wp;
   g.ws = w.ws;
   g.wz = w.wz;
@@ -1507,13 +1628,13 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, int M, void* 
   const int cm = tiles / tiles_n <= 4 ? 1 : 0;
   switch (w.form) {
     case TGOHIP_FORM_I4_SYM:
-      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
       break;
     case TGOHIP_FORM_I4_TGO:
-      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
       break;
     default:
-      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, st);
+      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
       break;
   }
   if (defer) *defer = splits > 1 ? splits : 0;
@@ -1533,25 +1654,28 @@ static int pipe_min_rows() {
   return v;
 }
 
-// The pipelined kernel serves the int4 packs and int8 with f16 activations;
-// f16 weights and f32 activations use gemm_kernel.
-static bool use_pipe(const PackedWeight& w, bool x_f32, int M) {
-  return !x_f32 && w.form != TGOHIP_FORM_F16 && M >= pipe_min_rows() && (w.K / 64) % 4 == 0 &&
+// The pipelined kernel serves the int4 packs and int8 with f16 activations
+// or activation pairs (XK_X2, the exact kernel); f16 weights and unsplit f32
+// activations use gemm_kernel.
+static bool use_pipe(const PackedWeight& w, int xk, int M) {
+  return xk != XK_F32 && w.form != TGOHIP_FORM_F16 && M >= pipe_min_rows() &&
+         (w.K / 64) % 4 == 0 &&
          (int64_t)M * w.K < ((int64_t)1 << 31);  // its activation offsets are 32-bit
 }
 
-// Workspace bytes a call needs for split-K partials: x_f32 < 0 bounds every
+// Workspace bytes a call needs for split-K partials: xk < 0 bounds every
 // activation type and epilogue; otherwise the bytes of exactly the call
-// gemm_enqueue makes with an f32 or f16 epilogue.
-size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int x_f32) {
+// gemm_enqueue makes over that activation type with an f32 or f16 epilogue.
+size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int xk) {
   if (M <= 0) return 0;  // nothing launches (and no tiles to divide the slots by)
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   int s;
-  if (x_f32 < 0) {
-    s = std::max(choose_splits(M, w.N, w.K, MW, ncu), pipe_launch(w, M, ncu, EPI_F32).splits);
-  } else if (use_pipe(w, x_f32 != 0, M)) {
-    s = pipe_launch(w, M, ncu, EPI_F32).splits;
-  } else if (use_gemv(w, x_f32 != 0, M, ncu)) {
+  if (xk < 0) {
+    s = std::max({choose_splits(M, w.N, w.K, MW, ncu), pipe_launch(w, M, ncu, EPI_F32, false).splits,
+                  pipe_launch(w, M, ncu, EPI_F32, true).splits});
+  } else if (use_pipe(w, xk, M)) {
+    s = pipe_launch(w, M, ncu, EPI_F32, xk == XK_X2).splits;
+  } else if (use_gemv(w, xk, M, ncu)) {
     s = 1;
   } else {
     s = choose_splits(M, w.N, w.K, MW, ncu);  // gemm_kernel's grid.z
@@ -1559,15 +1683,20 @@ size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int x_f32) {
   return s > 1 ? (size_t)s * split_plane_stride(M, w.N) * sizeof(float) : 0;
 }
 
-int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* y, int epi,
+int gemm_enqueue(const PackedWeight& w, const void* x, int xk, int M, void* y, int epi,
                  float* workspace, size_t ws_bytes, int ncu, hipStream_t st, int* defer) {
   if (defer) *defer = 0;
   if (M <= 0) return 0;
   if (defer && epi != EPI_F32 && epi != EPI_RESID)
     return fail(TGOHIP_ESTATE, "linear: only f32 and residual epilogues can defer split-K");
-  if (use_pipe(w, x_f32, M))
-    return gemm_pipe_enqueue(w, x, M, y, epi, workspace, ws_bytes, ncu, st, defer);
-  if (use_gemv(w, x_f32, M, ncu)) {
+  // a SwiGLU over activation-pair input stores a pair, and only then
+  if (xk == XK_X2 ? (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32) : epi == EPI_SWIGLU_X2)
+    return fail(TGOHIP_ESTATE, "linear: the activation-pair SwiGLU output goes with activation-pair input");
+  // an activation pair's lo plane follows its hi plane
+  const void* xlo = xk == XK_X2 ? (const void*)((const half_t*)x + (size_t)M * w.K) : nullptr;
+  if (use_pipe(w, xk, M))
+    return gemm_pipe_enqueue(w, x, xlo, M, y, epi, workspace, ws_bytes, ncu, st, defer);
+  if (use_gemv(w, xk, M, ncu)) {
     GemmArgs g{};
     g.x = x;
     g.wp = w.wp;
@@ -1589,8 +1718,10 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
   }
   const int MW = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
   const int splits = choose_splits(M, w.N, w.K, MW, ncu);
+  const bool split_a = xk != XK_F16;  // f32 or an activation pair: hi + lo planes
   GemmArgs g{};
   g.x = x;
+  g.xlo = xlo;
   g.wp = w.wp;
   g.ws = w.ws;
   g.wz = w.wz;
@@ -1608,13 +1739,13 @@ int gemm_enqueue(const PackedWeight& w, const void* x, bool x_f32, int M, void* 
   }
   const dim3 grid((unsigned)((w.N / 32 + 7) / 8), (unsigned)((M + MW - 1) / MW), (unsigned)splits);
   if (MW == 32) {
-    if (x_f32) launch_mw<32, true>(w.form, g, epi, grid, st);
+    if (split_a) launch_mw<32, true>(w.form, g, epi, grid, st);
     else launch_mw<32, false>(w.form, g, epi, grid, st);
   } else if (MW == 64) {
-    if (x_f32) launch_mw<64, true>(w.form, g, epi, grid, st);
+    if (split_a) launch_mw<64, true>(w.form, g, epi, grid, st);
     else launch_mw<64, false>(w.form, g, epi, grid, st);
   } else {
-    if (x_f32) launch_mw<128, true>(w.form, g, epi, grid, st);
+    if (split_a) launch_mw<128, true>(w.form, g, epi, grid, st);
     else launch_mw<128, false>(w.form, g, epi, grid, st);
   }
   if (defer) *defer = splits > 1 ? splits : 0;

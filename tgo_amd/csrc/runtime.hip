@@ -819,15 +819,18 @@ struct StepLaunch {
 };
 
 // A projection's algorithmic bytes (weights once, activations in, output out;
-// a residual add reads and writes h) and flops, 2*M*K*N.
-void gemm_algorithmic(const PackedWeight& w, int M, bool x_f32, int epi, double& bytes, double& flops) {
+// a residual add reads and writes h) and flops, 2*M*K*N. xk: XK_F16 (2 bytes
+// per activation), XK_F32 or XK_X2 (4).
+void gemm_algorithmic(const PackedWeight& w, int M, int xk, int epi, double& bytes, double& flops) {
   const double halves = (double)packed_scale_halves(w.form, w.K, w.N);
   bytes = (double)packed_payload_bytes(w.form, w.K, w.N) +
-          halves * 2 * (w.form == TGOHIP_FORM_I4_TGO ? 2 : 1) + (double)M * w.K * (x_f32 ? 4 : 2);
+          halves * 2 * (w.form == TGOHIP_FORM_I4_TGO ? 2 : 1) +
+          (double)M * w.K * (xk == XK_F16 ? 2 : 4);
   switch (epi) {
     case EPI_RESID: bytes += (double)M * w.N * 8; break;
     case EPI_SWIGLU_F16: bytes += (double)M * w.N / 2 * 2; break;
-    case EPI_SWIGLU_F32: bytes += (double)M * w.N / 2 * 4; break;
+    case EPI_SWIGLU_F32:
+    case EPI_SWIGLU_X2: bytes += (double)M * w.N / 2 * 4; break;
     case EPI_F16: bytes += (double)M * w.N * 2; break;
     default: bytes += (double)M * w.N * 4; break;
   }
@@ -928,8 +931,14 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                  sg.dev<int32_t>(c, o_seql), sg.dev<int32_t>(c, o_cu),
                  sg.dev<uint32_t>(c, o_len), d_ext, sg.dev<uint32_t>(c, o_pages),
                  (float*)c->part_o.p, (float*)c->part_ml.p};
+  // Precision mode 1 (tgo's f32 arithmetic): each projection's input is an
+  // activation pair written by its producer (rmsnorm, attention, the SwiGLU
+  // epilogue) and q is f32; mode 0: f16 activations and q.
   const bool f32act = c->precision == 1;
-  const int actf16 = f32act ? 0 : 1;
+  const int xk = f32act ? XK_X2 : XK_F16;
+  const int outf = f32act ? OUT_X2 : OUT_F16;
+  const int qf16 = f32act ? 0 : 1;
+  const int swiglu = f32act ? EPI_SWIGLU_X2 : EPI_SWIGLU_F16;
   const float scale = (float)(1.0 / std::sqrt((double)m.head_dim));  // session.go:821-823
   float* h = (float*)c->h.p;
   const size_t layer_kv = (size_t)c->kv_positions * m.kv_heads * kHeadDim;
@@ -954,12 +963,12 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     ab -= (double)plan.shared_positions * m.kv_heads * kHeadDim * 2 * 2;  // read once
     o.prof.flops[TGOHIP_PROF_ATTN] = 4.0 * kHeadDim * m.heads * pairs;
     const Layer& L0 = c->layers[0];
-    gemm_algorithmic(L0.qkv, Tw, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_QKV], o.prof.flops[TGOHIP_PROF_QKV]);
-    gemm_algorithmic(L0.wo, Tw, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_O], o.prof.flops[TGOHIP_PROF_O]);
-    gemm_algorithmic(L0.gateup, Tw, f32act, f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16,
-                     o.prof.bytes[TGOHIP_PROF_GATEUP], o.prof.flops[TGOHIP_PROF_GATEUP]);
-    gemm_algorithmic(L0.down, Tw, f32act, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
-    gemm_algorithmic(c->lm_head, B, f32act, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
+    gemm_algorithmic(L0.qkv, Tw, xk, EPI_F32, o.prof.bytes[TGOHIP_PROF_QKV], o.prof.flops[TGOHIP_PROF_QKV]);
+    gemm_algorithmic(L0.wo, Tw, xk, EPI_RESID, o.prof.bytes[TGOHIP_PROF_O], o.prof.flops[TGOHIP_PROF_O]);
+    gemm_algorithmic(L0.gateup, Tw, xk, swiglu, o.prof.bytes[TGOHIP_PROF_GATEUP],
+                     o.prof.flops[TGOHIP_PROF_GATEUP]);
+    gemm_algorithmic(L0.down, Tw, xk, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
+    gemm_algorithmic(c->lm_head, B, xk, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
                      o.prof.flops[TGOHIP_PROF_LMHEAD]);
     while (c->prof_ev.size() < (size_t)2 * m.layers * NK * 2) {
       // timing only: no system-scope fence (an L2 write-back each, which
@@ -993,10 +1002,10 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   int pend = 0;
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
-    launch_rmsnorm(h, nullptr, Tw, L.g_attn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    launch_rmsnorm(h, nullptr, Tw, L.g_attn, m.hidden, m.rms_eps, c->xn.p, outf, st, ws, pend, plane);
     int qkv_split = 0;
     if ((rc = mark(TGOHIP_PROF_QKV, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.qkv, c->xn.p, f32act, Tw, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
+    if ((rc = gemm_enqueue(L.qkv, c->xn.p, xk, Tw, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
                            &qkv_split)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
@@ -1006,35 +1015,34 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
-                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, actf16,
+                  c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, qf16,
                   derived ? (const float4_t*)c->rope.p : nullptr};
     launch_qk_rope_kv(qa, Tw, st);
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 0))) return rc;
-    if ((rc = attn_enqueue(plan, dp, c->q.p, actf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
-                           actf16, Tw, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
+    if ((rc = attn_enqueue(plan, dp, c->q.p, qf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
+                           outf, Tw, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 1))) return rc;
     if ((rc = mark(TGOHIP_PROF_O, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.wo, c->attn.p, f32act, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
+    if ((rc = gemm_enqueue(L.wo, c->attn.p, xk, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_O, l, 1))) return rc;
-    launch_rmsnorm(h, nullptr, Tw, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, actf16, st, ws, pend, plane);
+    launch_rmsnorm(h, nullptr, Tw, L.g_ffn, m.hidden, m.rms_eps, c->xn.p, outf, st, ws, pend, plane);
     if ((rc = mark(TGOHIP_PROF_GATEUP, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.gateup, c->xn.p, f32act, Tw, c->act.p,
-                           f32act ? EPI_SWIGLU_F32 : EPI_SWIGLU_F16, ws, wsb, c->ncu, st)))
+    if ((rc = gemm_enqueue(L.gateup, c->xn.p, xk, Tw, c->act.p, swiglu, ws, wsb, c->ncu, st)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_GATEUP, l, 1))) return rc;
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.down, c->act.p, f32act, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
+    if ((rc = gemm_enqueue(L.down, c->act.p, xk, Tw, h, EPI_RESID, ws, wsb, c->ncu, st, &pend)))
       return rc;
     if ((rc = mark(TGOHIP_PROF_DOWN, l, 1))) return rc;
   }
   // The last layer's split residual add is summed for the Last rows only (the
   // head reads nothing else); h keeps the rows without it.
   launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p,
-                 actf16, st, ws, pend, plane);
+                 outf, st, ws, pend, plane);
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 0))) return rc;
-  if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, f32act, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
+  if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, xk, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 1))) return rc;
   launch_argmax((float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, c->amax_part.p, st,
@@ -1242,6 +1250,11 @@ static PackedWeight* handle_of(tgohip_ctx* c, int handle) {
   return &it->second;
 }
 
+// TGOHIP_F32 / F16 / F16X2 as the kernels' activation kinds.
+static int xkind(int x_dtype) {
+  return x_dtype == TGOHIP_F32 ? XK_F32 : x_dtype == TGOHIP_F16X2 ? XK_X2 : XK_F16;
+}
+
 int tgohip_linear(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, void* y, int y_dtype) {
   PackedWeight* w = handle_of(c, handle);
   if (!w) return TGOHIP_EINVAL;
@@ -1250,7 +1263,8 @@ int tgohip_linear(tgohip_ctx* c, int handle, const void* x, int x_dtype, int M, 
   const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
   int rc = c->gemm_ws.ensure(ws + 256);
   if (rc) return rc;
-  return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
+  return gemm_enqueue(*w, x, xkind(x_dtype), M, y,
+                      y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
                       (float*)c->gemm_ws.p, c->gemm_ws.bytes, c->ncu, c->stream);
 }
 
@@ -1271,7 +1285,8 @@ int tgohip_linear_noalloc(tgohip_ctx* c, int handle, const void* x, int x_dtype,
                                    "and the static workspace holds " +
                                    std::to_string(kScratchBytes) + "; use tgohip_linear");
   if (!c->scratch) return fail(TGOHIP_ESTATE, "linear_noalloc: no workspace address for this device");
-  return gemm_enqueue(*w, x, x_dtype == TGOHIP_F32, M, y, y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
+  return gemm_enqueue(*w, x, xkind(x_dtype), M, y,
+                      y_dtype == TGOHIP_F16 ? EPI_F16 : EPI_F32,
                       (float*)c->scratch, kScratchBytes, c->ncu, c->stream);
 }
 
@@ -1279,7 +1294,7 @@ int tgohip_linear_workspace(tgohip_ctx* c, int handle, int x_dtype, int M, size_
   PackedWeight* w = handle_of(c, handle);
   if (!w) return TGOHIP_EINVAL;
   if (M < 0) return fail(TGOHIP_EINVAL, "linear_workspace: M is " + std::to_string(M));
-  *bytes = gemm_workspace_bytes(*w, M, c->ncu, x_dtype == TGOHIP_F32);
+  *bytes = gemm_workspace_bytes(*w, M, c->ncu, xkind(x_dtype));
   return 0;
 }
 
