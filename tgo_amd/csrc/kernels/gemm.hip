@@ -1489,6 +1489,17 @@ static int pipe_max_splits() {
   return v;
 }
 
+// TGOHIP_GEMM_EX_SPLITS (0: the rule below): split-K count for the exact
+// (activation-pair) kernel's unsplit-by-rule launches other than SwiGLU.
+static int pipe_ex_splits() {
+  static const int v = [] {
+    const char* e = getenv("TGOHIP_GEMM_EX_SPLITS");
+    const int n = e ? atoi(e) : 0;
+    return n >= 0 && n <= 8 ? n : 0;
+  }();
+  return v;
+}
+
 static int choose_pipe_splits(int tiles, int KS, int slots) {
   if (tiles <= 0 || tiles >= slots / 2) return 1;  // the partial sums would cost more than the fill gains
   int s = slots / tiles;              // one round of workgroups
@@ -1529,6 +1540,19 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
   tiles_n = (nb + 2 * nw - 1) / (2 * nw);
   tiles = tiles_n * rows;
   splits = choose_pipe_splits(tiles, w.K / 64, ncu * (8 / nw));
+  // The exact kernel's workgroups run three times the MFMAs: a launch that
+  // fills half to three quarters of the slots leaves most CUs one workgroup
+  // and the rest a second one, so it splits K to give every CU about two
+  // rounds (the O and down projections at 1152 rows, 288 tiles: 4 splits,
+  // 131 -> 118 and 377 -> 296 us with the standalone reduction).
+  if (ex && splits == 1 && 4 * tiles < 3 * ncu * (8 / nw)) {
+    splits = std::min(4, (2 * ncu * (8 / nw) + tiles - 1) / tiles);
+    while (splits > 1 && (w.K / 64) / splits < 8) splits--;
+  }
+  if (ex && pipe_ex_splits() > 0) {
+    splits = pipe_ex_splits();
+    while (splits > 1 && (w.K / 64) / splits < 8) splits--;
+  }
   if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) && tiles >= ncu / 2)
     splits = 1;
 }
