@@ -466,6 +466,19 @@ def recorded_traffic():
     return None
 
 
+def recorded_proj_traffic(step, proj):
+    """HBM bytes per dispatch of one projection (FETCH_SIZE + WRITE_SIZE, each scaled by a
+    copy probe) on this workload, as profiles/ records it -> (fetch, write) or None."""
+    path = os.path.join(ROOT, "profiles", "gemm_traffic_c4_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 5 and f[0] == "traffic" and f[1] == step and f[2] == proj:
+            return float(f[3]), float(f[4])
+    return None
+
+
 def cpu_baseline(st, pages, max_pages, out_tokens, form):
     """tgo's CPU path restated (oracle/, OpenMP) on one timed step: the step with 1
     and 2 layers, the per-layer time extrapolated to 36 layers."""
@@ -606,6 +619,9 @@ def main():
     achieved = (attn_bytes / max(launches, 1)) / (avg_attn_ms * 1e-3) / 1e9
     avg_gu_ms = gu_ms / max(gu_n, 1)
     gu_tflops = (gu_flops / max(gu_n, 1)) / (avg_gu_ms * 1e-3) / 1e12
+    # the committed counters were taken at the default arithmetic and weight form only
+    gu_traffic = recorded_proj_traffic("mixed", "gateup") \
+        if args.precision == 1 and args.form == tgo_amd.FORM_I4_SYM else None
     mfma_per_product = 3 if args.precision == 1 else 1
     rows_per_step = (total_pf + total_dc) / args.steps
     result = {
@@ -643,7 +659,11 @@ def main():
             "peak": MFMA_F16_PEAK,
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / MFMA_F16_PEAK, 4),
-            "traffic": None,
+            "traffic": round(sum(gu_traffic)) if gu_traffic else None,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE over 2 steps of this "
+                              "workload at this arithmetic, scaled by a 1 GiB copy probe "
+                              "(profiles/gemm_traffic_c4_pmc.txt)" if gu_traffic else None,
+            "algorithmic_bytes_per_launch": round(gu_bytes / max(gu_n, 1)),
             "flops_per_launch": round(gu_flops / max(gu_n, 1)),
             "flops_counted": "algorithmic, 2*M*K*N; the kernel executes %d f16 MFMAs per "
                              "product (%s)" % (mfma_per_product,
@@ -672,7 +692,8 @@ def main():
         "kernels": mixed_kernels,
         "decode_step": decode,
         "fast_path": fast,
-        "mfma_counters": recorded_mfma(),
+        "mfma_counters": recorded_mfma()
+        if args.precision == 1 and args.form == tgo_amd.FORM_I4_SYM else None,
     }
     ctx.close()
     if ach:

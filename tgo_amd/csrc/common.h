@@ -205,9 +205,12 @@ void launch_rope_table(const uint32_t* rowpos, int T, const double* inv_freq, fl
 // memory for the per-chunk partials (a size that also serves any call with
 // fewer rows).
 size_t argmax_scratch_bytes(int B, int V);
+// cidx != null: the logits hold `rows` compacted rows, those of the members
+// that worked; member b's is row cidx[b] (-1: extent 0, token -1 unless
+// keep_idle, margin 0). extents and zero_idle then play no part.
 void launch_argmax(float* logits, int B, int V, const uint32_t* extents, int32_t* out,
                    void* scratch, hipStream_t st, int keep_idle = 0, double* margin = nullptr,
-                   int zero_idle = 0);
+                   int zero_idle = 0, int rows = 0, const int32_t* cidx = nullptr);
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st);
 void launch_synth_absf16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,

@@ -408,22 +408,33 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(float* logi
   }
 }
 
-// extents == null treats every row as live.
+// extents == null treats every row as live. cidx != null: the logits hold
+// only the members that worked, compacted; member b's row is cidx[b] (-1 for
+// a member with extent 0: no token, margin 0, its logits row is not there).
 __global__ void argmax_final_kernel(const float* logits, int B, int V, int S,
                                     const uint32_t* extents, const Top2* part, int32_t* out,
-                                    int keep_idle, double* margin) {
+                                    int keep_idle, double* margin, const int32_t* cidx) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
-  const Top2* p = part + (size_t)b * S;
+  int rowi = b;
+  if (cidx) {
+    rowi = cidx[b];
+    if (rowi < 0) {
+      if (!keep_idle) out[b] = -1;
+      if (margin) margin[b] = 0.0;
+      return;
+    }
+  }
+  const Top2* p = part + (size_t)rowi * S;
   float t1 = p[0].t1, t2 = p[0].t2;
   int i1 = p[0].i1;
   for (int s = 1; s < S; s++) top2_merge(t1, t2, i1, p[s].t1, p[s].t2, p[s].i1);
   // x[0] itself, and NaN at x[0], are Go's starting point
-  const float* row = logits + (size_t)b * V;
+  const float* row = logits + (size_t)rowi * V;
   const float x0 = row[0];
   int r = i1;
   if (x0 != x0 || i1 == 0x7fffffff || !(t1 > x0)) r = 0;
-  const bool live = !extents || extents[b] != 0;
+  const bool live = cidx || !extents || extents[b] != 0;
   if (live) out[b] = r;
   else if (!keep_idle) out[b] = -1;
   if (margin) {
@@ -583,13 +594,20 @@ void launch_qk_rope_kv(const QKRopeArgs& a, int T, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(T, gy), dim3(256), 0, st, a);
 }
 void launch_argmax(float* logits, int B, int V, const uint32_t* extents, int32_t* out,
-                   void* scratch, hipStream_t st, int keep_idle, double* margin, int zero_idle) {
+                   void* scratch, hipStream_t st, int keep_idle, double* margin, int zero_idle,
+                   int rows, const int32_t* cidx) {
   if (B <= 0) return;
-  const int S = argmax_chunks(B, V);
-  hipLaunchKernelGGL(argmax_part_kernel, dim3(B, S), dim3(kArgmaxThreads), 0, st, logits, V, S,
-                     extents, zero_idle, (Top2*)scratch);
-  hipLaunchKernelGGL(argmax_final_kernel, dim3((B + 63) / 64), dim3(64), 0, st, logits, B, V, S,
-                     extents, (const Top2*)scratch, out, keep_idle, margin);
+  if (!cidx) rows = B;
+  if (rows > 0) {
+    const int S = argmax_chunks(rows, V);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(rows, S), dim3(kArgmaxThreads), 0, st, logits, V,
+                       S, cidx ? nullptr : extents, cidx ? 0 : zero_idle, (Top2*)scratch);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((B + 63) / 64), dim3(64), 0, st, logits, B, V, S,
+                       extents, (const Top2*)scratch, out, keep_idle, margin, cidx);
+  } else {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((B + 63) / 64), dim3(64), 0, st, logits, B, V, 1,
+                       extents, (const Top2*)scratch, out, keep_idle, margin, cidx);
+  }
 }
 void launch_synth_f16(uint64_t seed, uint64_t stream, size_t n, double sigma, uint16_t* out,
                       hipStream_t st) {

@@ -145,6 +145,9 @@ struct tgohip_ctx {
   DevBuf rope;  // [rows][32] float4: the rows' rotary cos and sin (rope_table)
   int rows_cap = 0, batch_cap = 0;
   int last_batch = 0;  // members of the last launched step (its margins are in `margin`)
+  // The head of the last launched step ran over the members that worked only:
+  // logits row i is member head_rows[i]'s (empty: one row per member).
+  std::vector<int32_t> head_rows;
   // pinned staging for per-step metadata
   void* pinned = nullptr;
   size_t pinned_bytes = 0;
@@ -904,6 +907,23 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
       if (s->extents[b] > 0 && s->last[b] >= (uint32_t)plan.claimed) inert = false;
     if (inert) Tw = plan.claimed;
   }
+  // The head's rows: only members that worked need logits (an idle member's
+  // row is zero and its token -1), so the final norm, the LM head and the
+  // greedy selection run over those, compacted: at C4 128-130 of 136 slots,
+  // and the LM head's 64-row tiles 2 instead of 3.
+  std::vector<uint32_t> head_last;
+  std::vector<int32_t> head_idx(B, -1);
+  c->head_rows.clear();
+  for (int b = 0; b < B; b++)
+    if (s->extents[b] > 0) {
+      head_idx[b] = (int32_t)c->head_rows.size();
+      c->head_rows.push_back(b);
+      head_last.push_back(s->last[b]);
+    }
+  const int nh = (int)c->head_rows.size();
+  const bool compact = nh > 0 && nh < B;
+  if (!compact) c->head_rows.clear();
+  const int HB = compact ? nh : B;  // rows of the head
   if ((rc = ensure_activations(c, Tw, B))) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
 
@@ -921,6 +941,8 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   const size_t o_items = sg.add(plan.items.data(), plan.items.size() * sizeof(AttnItem));
   const size_t o_comb = sg.add(plan.combines.data(), plan.combines.size() * sizeof(AttnCombine));
   const size_t o_seql = sg.add(plan.seqlist.data(), plan.seqlist.size() * sizeof(int32_t));
+  const size_t o_hlast = compact ? sg.add(head_last.data(), (size_t)nh * 4) : 0;
+  const size_t o_hidx = compact ? sg.add(head_idx.data(), (size_t)B * 4) : 0;
   if ((rc = sg.upload(c))) return rc;
   const hipStream_t st = c->stream;
   TGOHIP_HIP(hipEventRecord(o.ev_begin, st));
@@ -968,7 +990,7 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     gemm_algorithmic(L0.gateup, Tw, xk, swiglu, o.prof.bytes[TGOHIP_PROF_GATEUP],
                      o.prof.flops[TGOHIP_PROF_GATEUP]);
     gemm_algorithmic(L0.down, Tw, xk, EPI_RESID, o.prof.bytes[TGOHIP_PROF_DOWN], o.prof.flops[TGOHIP_PROF_DOWN]);
-    gemm_algorithmic(c->lm_head, B, xk, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
+    gemm_algorithmic(c->lm_head, HB, xk, EPI_F32, o.prof.bytes[TGOHIP_PROF_LMHEAD],
                      o.prof.flops[TGOHIP_PROF_LMHEAD]);
     while (c->prof_ev.size() < (size_t)2 * m.layers * NK * 2) {
       // timing only: no system-scope fence (an L2 write-back each, which
@@ -1039,14 +1061,15 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   }
   // The last layer's split residual add is summed for the Last rows only (the
   // head reads nothing else); h keeps the rows without it.
-  launch_rmsnorm(h, sg.dev<uint32_t>(c, o_last), B, c->g_final, m.hidden, m.rms_eps, c->lastn.p,
-                 outf, st, ws, pend, plane);
+  launch_rmsnorm(h, sg.dev<uint32_t>(c, compact ? o_hlast : o_last), HB, c->g_final, m.hidden,
+                 m.rms_eps, c->lastn.p, outf, st, ws, pend, plane);
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 0))) return rc;
-  if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, xk, B, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
+  if ((rc = gemm_enqueue(c->lm_head, c->lastn.p, xk, HB, c->logits.p, EPI_F32, ws, wsb, c->ncu, st)))
     return rc;
   if ((rc = mark(TGOHIP_PROF_LMHEAD, 0, 1))) return rc;
   launch_argmax((float*)c->logits.p, B, m.vocab, d_ext, (int32_t*)c->argmax.p, c->amax_part.p, st,
-                o.keep_idle, (double*)c->margin.p, 1);
+                o.keep_idle, (double*)c->margin.p, 1, HB,
+                compact ? sg.dev<int32_t>(c, o_hidx) : nullptr);
   TGOHIP_HIP(hipEventRecord(o.ev_end, st));
   TGOHIP_HIP(hipGetLastError());
   c->last_batch = B;
@@ -1091,8 +1114,17 @@ int tgohip_step(tgohip_ctx* c, const tgohip_batch_step* s, float* logits_out, in
   TGOHIP_HIP(hipEventSynchronize(c->ev1));
   const auto t_dev = clk::now();
   const tgohip_model_cfg& m = c->cfg;
-  if (logits_out)
+  if (logits_out && c->head_rows.empty()) {
     TGOHIP_HIP(hipMemcpy(logits_out, c->logits.p, (size_t)s->batch * m.vocab * 4, hipMemcpyDeviceToHost));
+  } else if (logits_out) {
+    // compacted head rows: each member that worked gets its row, idle members zeros
+    const size_t V = (size_t)m.vocab;
+    std::vector<float> rows(c->head_rows.size() * V);
+    TGOHIP_HIP(hipMemcpy(rows.data(), c->logits.p, rows.size() * 4, hipMemcpyDeviceToHost));
+    memset(logits_out, 0, (size_t)s->batch * V * 4);
+    for (size_t i = 0; i < c->head_rows.size(); i++)
+      memcpy(logits_out + (size_t)c->head_rows[i] * V, rows.data() + i * V, V * 4);
+  }
   if (argmax_out) TGOHIP_HIP(hipMemcpy(argmax_out, c->argmax.p, (size_t)s->batch * 4, hipMemcpyDeviceToHost));
   const auto t_end = clk::now();
   if ((rc = profile_collect(c, 0, o.prof))) return rc;

@@ -16,10 +16,11 @@
         per (kernel, grid size): dispatches and the median and mean duration, so
         launches of one kernel at different shapes stay apart (from --kernel-trace
         --output-format csv).
-    python -m tgo_amd.prof pmcproj <fetch_counter_collection.csv> <write_counter_collection.csv> [probe_mib]
+    python -m tgo_amd.prof pmcproj <fetch_counter_collection.csv> <write_counter_collection.csv> [probe_mib [label]]
         the same scaled FETCH_SIZE / WRITE_SIZE per projection of the step (labelled as
         by mfma), with the fetch over the projection's int4-sym weight bytes at the C4
-        (Qwen3-8B) shapes.
+        (Qwen3-8B) shapes; with a label, also one line per projection
+        "traffic <label> <proj> <fetch bytes> <write bytes>" per dispatch.
     python -m tgo_amd.prof pmc <fetch_counter_collection.csv> <write_counter_collection.csv>
         per-kernel mean FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by
         what the same counter reads for the copy-probe dispatch (torch.neg over a
@@ -97,7 +98,7 @@ C4_WEIGHT_BYTES = {"qkv": 4096 * 6144 * 0.5625, "o": 4096 * 4096 * 0.5625,
                    "lm_head": 4096 * 151936 * 0.5625}
 
 
-def pmcproj(fetch_path, write_path, probe_mib):
+def pmcproj(fetch_path, write_path, probe_mib, label=None):
     probe = "copy-probe (torch.neg f32)"
     known_kib = probe_mib * 1024.0
     res = {}
@@ -125,6 +126,13 @@ def pmcproj(fetch_path, write_path, probe_mib):
         fm, wm = sum(f) / len(f) / 1e6, sum(w) / len(w) / 1e6
         wb = C4_WEIGHT_BYTES[lab] / 1e6
         print("%-8s %6d %12.2f %12.2f %14.2f %12.3f" % (lab, len(f), fm, wm, wb, fm / wb))
+    if label:
+        # machine-readable: HBM bytes per dispatch (fetch + write), for bench.py's roofline
+        for lab in ("qkv", "o", "gateup", "down", "lm_head"):
+            f = res["FETCH_SIZE"].get(lab)
+            w = res["WRITE_SIZE"].get(lab)
+            if f and w:
+                print("traffic %s %s %.0f %.0f" % (label, lab, sum(f) / len(f), sum(w) / len(w)))
 
 
 MFMA_PEAK_TFLOPS = 2500.0
@@ -209,7 +217,8 @@ if __name__ == "__main__":
     elif sys.argv[1] == "mfma":
         mfma(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "pmcproj":
-        pmcproj(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
+        pmcproj(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024,
+                sys.argv[5] if len(sys.argv) > 5 else None)
     elif sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
     else:
