@@ -81,7 +81,7 @@ int tgohip_sync(tgohip_ctx* ctx);
  * stream); tgohip_use_own_stream returns to it. */
 int tgohip_set_stream(tgohip_ctx* ctx, void* stream);
 int tgohip_use_own_stream(tgohip_ctx* ctx);
-/* Arithmetic of the step. 1 is tgo's CPU path (nn/blocks.go:13-21): every
+/* Arithmetic of the step. 1 (the default) is tgo's CPU path (nn/blocks.go:13-21): every
  * projection multiplies the f32 activation (carried as an f16 high + low pair,
  * ~22 bits) by the unrounded dequantized weight (carried as an exact f16
  * high + low pair), f32 accumulate -- three f16 MFMAs per product -- and

@@ -99,16 +99,16 @@ def test_c4_step_matches_the_cpu_path(torch_gpu):
         ctx.kv_synth(bench.SEED, 1.0, min(pool, wl.used_positions + 64 * bench.CHUNK))
         cpu = cpu_model(cfg, form, pool, bench.SEED)
         copy_pool(ctx, cpu, LAYERS, cfg["kv_heads"], pool)
-        produced, prefill, decodes, _ = wl.sched.step()  # mode 0, the bench's precision
+        produced, prefill, decodes, _ = wl.sched.step()  # mode 1, the default
         assert (prefill, decodes) == (2 * bench.CHUNK, bench.DECODERS)
         st, pages, maxp = wl.sched.last_step()
         assert len(st["ids"]) == 1152 and len(st["lengths"]) == bench.SLOTS
         want = cpu.step(st, pages, maxp, layers=LAYERS)
         near, decisions = [], 0
-        for precision in (0, 1):
+        for precision in (1, 0):
             ctx.set_precision(precision)
             logits, ids, _ = ctx.step(st, pages, maxp)
-            if precision == 0:
+            if precision == 1:
                 for slot, tok, done in produced:
                     assert tok == int(ids[slot]), (slot, tok, int(ids[slot]))
             n, nt = compare(logits, ids, want, st["extents"], "C4 precision %d" % precision)
@@ -142,10 +142,10 @@ def test_c4_decode_step_matches_the_cpu_path(torch_gpu):
         assert len(st["ids"]) == bench.DECODERS
         want = cpu.step(st, pages, maxp, layers=LAYERS)
         near, decisions = [], 0
-        for precision in (0, 1):
+        for precision in (1, 0):
             ctx.set_precision(precision)
             logits, ids, _ = ctx.step(st, pages, maxp)
-            if precision == 0:
+            if precision == 1:
                 for slot, tok, done in produced:
                     assert tok == int(ids[slot]), (slot, tok, int(ids[slot]))
             n, nt = compare(logits, ids, want, st["extents"], "C4 decode precision %d" % precision)

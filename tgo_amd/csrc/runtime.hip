@@ -136,7 +136,7 @@ struct tgohip_ctx {
   half_t* kc = nullptr;
   half_t* vc = nullptr;
   int kv_positions = 0;
-  int precision = 0;  // 0: f16 activations into MFMA, 1: f32 activations (hi+lo)
+  int precision = 1;  // 1 (default): tgo's f32 arithmetic (hi+lo pairs), 0: f16 operands
   int cascade = 0;    // minimum sequences sharing a prefix for prefix-shared attention (0: off)
   // activations and workspaces
   DevBuf h, xn, qkv, q, attn, act, lastn, logits, argmax, margin, meta, gemm_ws, part_o, part_ml;
