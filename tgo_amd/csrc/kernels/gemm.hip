@@ -235,11 +235,11 @@ __device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I4_SYM>& r, i
   const half2_t sp = {s, s};
   const uint32_t w = word_of(r.p, j), w8 = w >> 8;
   const half2_t b0 = {(half_t)1032.f, (half_t)1032.f}, b1 = {(half_t)72.f, (half_t)72.f};
-  // q - 8 exactly, as in deq_i4_sym
-  const half2_t d[4] = {as_h2((w & 0x000F000Fu) | 0x64006400u) - b0,
-                        as_h2((w & 0x00F000F0u) | 0x54005400u) - b1,
-                        as_h2((w8 & 0x000F000Fu) | 0x64006400u) - b0,
-                        as_h2((w8 & 0x00F000F0u) | 0x54005400u) - b1};
+  // q - 8 exactly, as in deq_i4_sym (masks in registers: one v_and_or_b32 each)
+  uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, g0 = 0x64006400u, g1 = 0x54005400u;
+  asm("" : "+v"(m0), "+v"(m1), "+v"(g0), "+v"(g1));
+  const half2_t d[4] = {as_h2((w & m0) | g0) - b0, as_h2((w & m1) | g1) - b1,
+                        as_h2((w8 & m0) | g0) - b0, as_h2((w8 & m1) | g1) - b1};
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     half2_t h, l;
@@ -255,11 +255,12 @@ __device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I4_TGO>& r, i
   s.u = r.s[j];
   z.u = r.z[j];
   const uint32_t w = word_of(r.p, j);
+  uint32_t m0 = 0x000F000Fu, g0 = 0x64006400u;
+  asm("" : "+v"(m0), "+v"(g0));
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     // (1024 + q) - (1024 + z) = q - z exactly
-    const half2_t d = as_h2(((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u) -
-                      half2_t{z.h[2 * i], z.h[2 * i + 1]};
+    const half2_t d = as_h2(((w >> (4 * i)) & m0) | g0) - half2_t{z.h[2 * i], z.h[2 * i + 1]};
     half2_t h, l;
     split_pair(d, half2_t{s.h[2 * i], s.h[2 * i + 1]}, h, l);
     pack_pair(hi, i, h);
@@ -274,11 +275,13 @@ __device__ __forceinline__ void bfrag_split(const BRaw<TGOHIP_FORM_I8>& r, int j
   U16B s;
   s.u = r.s[j];
   const half2_t bias = {(half_t)1152.f, (half_t)1152.f};
+  uint32_t m0 = 0x00FF00FFu, g0 = 0x64006400u;
+  asm("" : "+v"(m0), "+v"(g0));
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     // (1024 + q + 128) - 1152 = q exactly
-    const half2_t dl = as_h2((ws[u] & 0x00FF00FFu) | 0x64006400u) - bias;
-    const half2_t dh = as_h2(((ws[u] >> 8) & 0x00FF00FFu) | 0x64006400u) - bias;
+    const half2_t dl = as_h2((ws[u] & m0) | g0) - bias;
+    const half2_t dh = as_h2(((ws[u] >> 8) & m0) | g0) - bias;
     half2_t h, l;
     split_pair(dl, half2_t{s.h[4 * u], s.h[4 * u + 1]}, h, l);
     pack_pair(hi, 2 * u, h);
@@ -818,7 +821,7 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
               acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfcl[b], acc[mb][b], 0, 0, 0);
         }
         if constexpr (EX) {
-          // 12 MFMAs (64-row tiles), 4 LDS reads, the B pairs' ~34 VALU
+          // 12 MFMAs (64-row tiles), 4 LDS reads, the B pairs' 36 VALU
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -850,9 +853,11 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
         }
         if (j == 1) {
           __builtin_amdgcn_sched_barrier(0);
-          // vmcnt(2 * B loads + A DMA + scale DMA), expcnt untouched, lgkmcnt(0)
-          static_assert(2 * pipe_b_loads<FORM>() + AP * ACH + 1 < 16, "vmcnt fits 4 bits");
-          __builtin_amdgcn_s_waitcnt((2 * pipe_b_loads<FORM>() + AP * ACH + (LS ? 1 : 0)) | (7 << 4));
+          // vmcnt(2 * B loads + A DMA + scale DMA), expcnt untouched, lgkmcnt(0);
+          // vmcnt's low 4 bits sit at 3:0 and its high 2 at 15:14
+          constexpr int VMC = 2 * pipe_b_loads<FORM>() + AP * ACH + (LS ? 1 : 0);
+          static_assert(VMC < 64, "vmcnt fits 6 bits");
+          __builtin_amdgcn_s_waitcnt((VMC & 15) | ((VMC >> 4) << 14) | (7 << 4));
           asm volatile("" ::: "memory");
           __builtin_amdgcn_s_barrier();
           asm volatile("" ::: "memory");
