@@ -152,27 +152,69 @@ def test_linear_is_deterministic_and_row_independent(ctx, torch_gpu):
         ctx.weight_free(h)
 
 
+def sym_codes_and_columns(K, N, seed, stream, sigma, cols):
+    """Host int4-sym codes (the oracle's seeded generator) and the oracle's f32
+    dequantization of the sampled columns: the codes go up through the product's
+    upload and repack, the reference never touches the device's weights."""
+    qw, sc = oracle.synth_int4_sym(seed, stream, K, N, sigma)
+    wc = oracle.dequant(3, K, len(cols), np.ascontiguousarray(qw[:, cols]),
+                        np.ascontiguousarray(sc[:, cols]))
+    return qw, sc, wc
+
+
 @pytest.mark.parametrize("KN", [(4096, 12288), (12288, 4096), (4096, 6144)])
 def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
     """BASELINE config 3 shapes (int4 symmetric, group 32 along K) at M = 1..1024,
-    checked on sampled columns against the f64 product of the same operands."""
+    checked on sampled columns against the f64 product of the same f16 operands, the
+    weights dequantized by the oracle from the host's codes."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN
-    h = ctx.weight_synth(3, K, N, 42, 5, 0.02)
+    cols = np.arange(0, N, N // 64)
+    qw, sc, wc = sym_codes_and_columns(K, N, 42, 5, 0.02, cols)
+    w16 = torch.from_numpy(wc.astype(np.float16).astype(np.float64)).cuda()
+    h = ctx.weight_upload(3, K, N, qw, sc)
     try:
-        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
-        ctx.dequant_f16(h, wf)
+        dcols = torch.from_numpy(cols).cuda()
         for M in (1, 8, 64, 256, 1024):
             x = torch.randn(M, K, device="cuda").half()
             y = torch.empty(M, N, device="cuda")
             ctx.linear(h, x, M, y, x_dtype=tgo_amd.F16)
             torch.cuda.synchronize()
-            cols = torch.arange(0, N, N // 64, device="cuda")
-            ref = x.double() @ wf[:, cols].double()
-            mag = x.double().abs() @ wf[:, cols].double().abs()
+            ref = x.double() @ w16
+            mag = x.double().abs() @ w16.abs()
             tol = 4 * (K ** 0.5) * 2.0 ** -24 * mag
-            assert bool(((y[:, cols].double() - ref).abs() <= tol).all()), M
+            assert bool(((y[:, dcols].double() - ref).abs() <= tol).all()), M
+    finally:
+        ctx.weight_free(h)
+
+
+@pytest.mark.parametrize("KN", [(4096, 12288), (12288, 4096), (4096, 6144)])
+def test_c3_shapes_tgo_arithmetic_sampled_columns(ctx, torch_gpu, KN):
+    """The same shapes in tgo's arithmetic (activation pairs, the exact kernel) at the
+    step's row counts, against the f64 product of the f32 activations and the oracle's
+    f32 dequantized weights, AccumF32 + 2^-22."""
+    torch = torch_gpu
+    import tgo_amd
+    K, N = KN
+    cols = np.arange(0, N, N // 64)
+    qw, sc, wc = sym_codes_and_columns(K, N, 43, 6, 0.02, cols)
+    w64 = torch.from_numpy(wc.astype(np.float64)).cuda()
+    h = ctx.weight_upload(3, K, N, qw, sc)
+    try:
+        dcols = torch.from_numpy(cols).cuda()
+        for M in (128, 1152, 1280):
+            x = torch.randn(M, K, device="cuda")
+            hi = x.half()
+            lo = (x - hi.float()).half()
+            xp = torch.cat([hi.reshape(-1), lo.reshape(-1)])
+            y = torch.empty(M, N, device="cuda")
+            ctx.linear(h, xp, M, y, x_dtype=tgo_amd.F16X2)
+            torch.cuda.synchronize()
+            ref = x.double() @ w64
+            mag = x.double().abs() @ w64.abs()
+            tol = (4 * (K ** 0.5) * 2.0 ** -24 + 2.0 ** -22) * mag
+            assert bool(((y[:, dcols].double() - ref).abs() <= tol).all()), M
     finally:
         ctx.weight_free(h)
 
@@ -216,18 +258,19 @@ def test_small_m_kernel_against_its_operands(ctx, torch_gpu, KN):
     """The small-M kernels (at most 32 rows; 1-8 rows on the 16x16x32 pairing) at the
     8B projection shapes, 16 waves per column block (QKV [4096, 6144], down [12288, 4096])
     and 4 (gate/up [4096, 24576], LM head [4096, 151936]): f32 output on sampled columns
-    against the f64 product of the same operands; repeated calls bit-equal; the f16 output
-    is the f16 rounding of the same sums."""
+    against the f64 product of the same operands (the weights dequantized by the oracle
+    from the host's codes); repeated calls bit-equal; the f16 output is the f16 rounding of
+    the same sums."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN
-    h = ctx.weight_synth(3, K, N, 11, 5, 0.02)
+    ncols = np.arange(0, N, max(1, N // 96))
+    qw, sc, wcols = sym_codes_and_columns(K, N, 11, 5, 0.02, ncols)
+    h = ctx.weight_upload(3, K, N, qw, sc)
+    del qw, sc
     try:
-        cols = torch.arange(0, N, max(1, N // 96), device="cuda")
-        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
-        ctx.dequant_f16(h, wf)
-        wc = wf[:, cols].double()
-        del wf
+        cols = torch.from_numpy(ncols).cuda()
+        wc = torch.from_numpy(wcols.astype(np.float16).astype(np.float64)).cuda()
         for M in (1, 3, 8, 9, 32):
             print("small-M linear [%d,%d] M=%d" % (K, N, M), flush=True)
             x = torch.randn(M, K, device="cuda").half()
@@ -258,16 +301,17 @@ def test_large_m_tiles_ragged_edges(ctx, torch_gpu, M, KN, form):
     chip; int8 and tgo's int4 with their scales through LDS): partial row and
     column tiles and every column checked against the f64 product of the same
     f16 operands. N = 4096 and 3712 (116 column blocks: the last 512-column
-    tile holds 4) run 128-row tiles 8 waves wide."""
+    tile holds 4) run 128-row tiles 8 waves wide. The weights are the host's codes, the
+    reference's dequantized by the oracle."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN
     if form == 2 and N % 128:
         N = 512  # tgo's int4 groups run along N in 128s
-    h = ctx.weight_synth(form, K, N, 17, M, 0.02)
+    wd, _ = make_weight(form, K, N, np.random.default_rng(17 + M))
+    wf = torch.from_numpy(deq(form, K, N, wd).astype(np.float16)).cuda()
+    h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
     try:
-        wf = torch.empty((K, N), dtype=torch.float16, device="cuda")
-        ctx.dequant_f16(h, wf)
         x = torch.randn(M, K, device="cuda").half()
         y = torch.full((M, N), float("nan"), device="cuda")
         ctx.linear(h, x, M, y, x_dtype=tgo_amd.F16)
