@@ -55,6 +55,12 @@ PREFILLING = 2
 C5 = dict(layers=64, hidden=5120, heads=64, kv_heads=8, head_dim=128, ffn=25600, vocab=151936,
           rms_eps=1e-6, rope_theta=1e6, block=16)
 C5_PREFIX = 2048        # tokens every sequence begins with (128 shared pages)
+# BASELINE config 1 (bench.py --config c1): Qwen3-0.6B-shaped, f16 weights, one step
+C1 = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, ffn=3072, vocab=151936,
+          rms_eps=1e-6, rope_theta=1e6, block=16)
+C1_CONTEXTS = (37, 300, 511)  # the decoding sequences' contexts
+C1_CHUNK = 64                 # the fresh sequence's prefill chunk
+C1_POOL = 4096
 C5_DECODERS = 256
 C5_CHUNK = 1024
 C5_POOL = 330_000       # positions (86 GB of f16 K+V at 64 layers)
@@ -89,10 +95,11 @@ def parse():
                    help="synchronous steps (tgo's Batch.step: pack, submit, wait, read back); "
                         "the default overlaps the host's scheduling of step k+1 with the "
                         "device's step k (the same steps and tokens)")
-    p.add_argument("--config", default="c4", choices=["c4", "c5"],
+    p.add_argument("--config", default="c4", choices=["c4", "c5", "c1"],
                    help="c4 (default): the headline workload; c5: BASELINE config 5, Qwen3-32B "
                         "int8 with a 2048-token prefix shared by 256 sequences (prefix-shared "
-                        "attention on)")
+                        "attention on); c1: BASELINE config 1, Qwen3-0.6B f16, its one step "
+                        "(3 decodes + a 64-token chunk) replayed, tgo's CPU path timed beside it")
     p.add_argument("--cascade", type=int, default=2,
                    help="config 5: group decode rows whose page tables share a prefix when at "
                         "least this many do (0: off, every sequence reads its own prefix)")
@@ -107,9 +114,9 @@ def parse():
                         "many MiB: the known-size dispatch that scales the HBM byte counters")
     args = p.parse_args()
     if args.steps is None:
-        args.steps = 10 if args.config == "c5" else 200
+        args.steps = {"c5": 10, "c1": 500}.get(args.config, 200)
     if args.warmup is None:
-        args.warmup = 3 if args.config == "c5" else 10
+        args.warmup = {"c5": 3, "c1": 20}.get(args.config, 10)
     return args
 
 
@@ -395,6 +402,89 @@ def run_c5(args, tgo_amd):
     }
 
 
+def run_c1(args, tgo_amd):
+    """Qwen3-0.6B-shaped, random-init f16 weights N(0, 0.02); one
+    continuous-batching step of 3 decoding sequences (contexts 37, 300, 511) plus a
+    64-token chunk of a fresh sequence, page 16. The step is built by the library
+    Scheduler and replayed through tgohip_step (rewriting its K/V rows with the same
+    values is idempotent) with tgohip_step, which waits for the step and reads back the
+    greedy tokens: ms_per_step is the synchronous step's latency. The CPU restatement of
+    tgo's path steps the same ports."""
+    c = C1
+    ctx = tgo_amd.Context(0)
+    ctx.set_precision(args.precision)
+    ctx.config(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"],
+               c["vocab"], c["rms_eps"], c["rope_theta"], c["block"])
+    ctx.kv_alloc(C1_POOL)
+    ctx.synth_weights(SEED, tgo_amd.FORM_F16, 0.02)
+    rng = np.random.default_rng(SEED)
+    sched = tgo_amd.Scheduler(ctx, 4, chunk=C1_CHUNK, reserve=16, max_rows=C1_CHUNK + 3)
+    for n in C1_CONTEXTS:
+        sched.admit_prefilled([int(t) for t in rng.integers(0, c["vocab"], n)],
+                              int(rng.integers(0, c["vocab"])), reserve=16)
+    sched.admit([int(t) for t in rng.integers(0, c["vocab"], C1_CHUNK)], reserve=16)
+    ctx.kv_synth(SEED, 1.0, C1_POOL)
+    _, prefill, decodes, _ = sched.step()
+    assert (prefill, decodes) == (C1_CHUNK, len(C1_CONTEXTS)), (prefill, decodes)
+    st, pages, maxp = sched.last_step()
+    members = len(st["lengths"])
+    for _ in range(args.warmup):
+        ctx.step(st, pages, maxp, want_logits=False)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.step(st, pages, maxp, want_logits=False)
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ms = 1e3 * el / args.steps
+    ctx.close()
+    d, f, L, V = c["hidden"], c["ffn"], c["layers"], c["vocab"]
+    qw, kw = c["heads"] * 128, c["kv_heads"] * 128
+    weights = 2.0 * (L * (d * (qw + 2 * kw) + qw * d + 2 * d * f + f * d) + d * V)
+    gbs = weights / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "step latency and output tok/s, Qwen3-0.6B f16 one continuous-batching step, "
+                  "1 MI355X",
+        "value": round(members / (ms * 1e-3), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.precision == 0 else "f32 (f16 hi+lo operand pairs)",
+        "data": "synthetic (seeded random-init f16 weights, seeded token ids, synthetic KV)",
+        "config": {"workload": "BASELINE config 1: Qwen3-0.6B-shaped f16 (28 layers, hidden 1024, "
+                               "16 q / 8 kv heads, MLP 3072, vocab 151936); 3 decodes at contexts "
+                               "37/300/511 + a 64-token chunk of a fresh sequence, page 16; the "
+                               "one step replayed (%d rows, %d members)" % (len(st["ids"]), members)},
+        "roofline": {"kernel": "the whole step (weights once: the 28 layers' f16 projections "
+                               "and the LM head)",
+                     "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": round(weights)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        import oracle
+        cpu = oracle.CPUModel(L, d, c["heads"], c["kv_heads"], c["head_dim"], f, V, c["rms_eps"],
+                              c["rope_theta"], c["block"], C1_POOL)
+        cpu.synth(SEED, tgo_amd.FORM_F16, 0.02)
+        cpu.step(st, pages, maxp)  # first touch of its pool and weights
+        t0 = time.perf_counter()
+        cpu.step(st, pages, maxp)
+        cs = time.perf_counter() - t0
+        cpu.close()
+        out["cpu_baseline"] = dict(value=round(members / cs, 3), unit="tok/s",
+                                   cores=int(oracle.lib.orc_num_threads()), kind="port",
+                                   sample="the same step (%d rows, all 28 layers) stepped once by "
+                                          "the CPU restatement after a first-touch step: %.3f s; "
+                                          "KV contents zero" % (len(st["ids"]), cs))
+    return out
+
+
 def kernel_table(ctx, tgo, kinds):
     """Per-launch means of the profiled kernel kinds: duration, algorithmic bytes and flops,
     and the fractions of the HBM and dense f16 MFMA peaks they reach."""
@@ -576,6 +666,9 @@ def main():
     import tgo_amd
     if args.config == "c5":
         print(json.dumps(run_c5(args, tgo_amd)), flush=True)
+        return
+    if args.config == "c1":
+        print(json.dumps(run_c1(args, tgo_amd)), flush=True)
         return
     t_setup = time.perf_counter()
     ctx = tgo_amd.Context(0)
