@@ -189,11 +189,11 @@ def test_c3_shapes_sampled_columns(ctx, torch_gpu, KN):
         ctx.weight_free(h)
 
 
-@pytest.mark.parametrize("KN", [(4096, 12288), (12288, 4096), (4096, 6144)])
+@pytest.mark.parametrize("KN", [(4096, 12288), (12288, 4096), (4096, 6144), (4096, 24576)])
 def test_c3_shapes_tgo_arithmetic_sampled_columns(ctx, torch_gpu, KN):
     """The same shapes in tgo's arithmetic (activation pairs, the exact kernel) at the
     step's row counts, against the f64 product of the f32 activations and the oracle's
-    f32 dequantized weights, AccumF32 + 2^-22."""
+    f32 dequantized weights, AccumF32 + 2^-22; [4096, 24576] is the fused gate/up."""
     torch = torch_gpu
     import tgo_amd
     K, N = KN
