@@ -21,6 +21,10 @@
         by mfma), with the fetch over the projection's int4-sym weight bytes at the C4
         (Qwen3-8B) shapes; with a label, also one line per projection
         "traffic <label> <proj> <fetch bytes> <write bytes>" per dispatch.
+    python -m tgo_amd.prof sq <pass_a_counter_collection.csv> <pass_b_counter_collection.csv> <label>
+        per projection: the MFMA unit's busy fraction of the SIMD cycles, the cycles
+        other VALU instructions issue, how many of those co-issue with a busy MFMA unit,
+        and the cycles with neither (from the counters named in sq's docstring).
     python -m tgo_amd.prof pmc <fetch_counter_collection.csv> <write_counter_collection.csv>
         per-kernel mean FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by
         what the same counter reads for the copy-probe dispatch (torch.neg over a
@@ -209,6 +213,49 @@ def mfma(path, label):
             print("mfma %s %s %.1f %.4f %.4f" % (label, lab, tflops, tflops / MFMA_PEAK_TFLOPS, busy))
 
 
+def _per_label(path):
+    """Counter sums, dispatch counts and durations per projection label."""
+    per = collections.defaultdict(dict)
+    for r in csv.DictReader(open(path)):
+        d = per[int(r["Dispatch_Id"])]
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        d["name"] = short(r["Kernel_Name"])
+        d["ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+    ids = sorted(per)
+    out = collections.defaultdict(lambda: collections.defaultdict(float))
+    for i, lab in zip(ids, label_projections([per[i]["name"] for i in ids])):
+        if lab is None:
+            continue
+        for k, v in per[i].items():
+            if k != "name":
+                out[lab][k] += v
+        out[lab]["n"] += 1
+    return out
+
+
+def sq(path_a, path_b, label):
+    """Where a projection's SIMD cycles go, from two passes: A = SQ_VALU_MFMA_BUSY_CYCLES,
+    SQ_VALU_MFMA_COEXEC_CYCLES, SQ_INSTS_VALU, GRBM_GUI_ACTIVE; B = SQ_INSTS_MFMA,
+    GRBM_GUI_ACTIVE. SIMD cycles = GRBM_GUI_ACTIVE / 8 x 1024. SQ_INSTS_VALU counts the
+    MFMAs too; each other VALU instruction issues over 4 cycles (a wave64 on a 16-lane
+    SIMD). co-issued = cycles with the MFMA unit busy and a VALU instruction issued."""
+    a, b = _per_label(path_a), _per_label(path_b)
+    print("%-8s %5s %9s %10s %10s %11s %10s %8s" % (
+        "proj", "disp", "avg_us", "mfma_busy", "valu_issue", "co-issued", "valu_only", "neither"))
+    for lab in ("qkv", "o", "gateup", "down", "lm_head"):
+        if lab not in a or lab not in b:
+            continue
+        A, B = a[lab], b[lab]
+        cyc = A["GRBM_GUI_ACTIVE"] / XCDS * SIMDS
+        busy = A["SQ_VALU_MFMA_BUSY_CYCLES"] / cyc
+        coex = A["SQ_VALU_MFMA_COEXEC_CYCLES"] / cyc
+        valu = 4 * (A["SQ_INSTS_VALU"] / A["n"] - B["SQ_INSTS_MFMA"] / B["n"]) * A["n"] / cyc
+        only = max(0.0, valu - coex)
+        print("%-8s %5d %9.2f %10.3f %10.3f %11.3f %10.3f %8.3f" % (
+            lab, A["n"], A["ns"] / A["n"] / 1e3, busy, valu, coex, only, max(0.0, 1 - busy - only)))
+        print("sq %s %s %.4f %.4f %.4f %.4f" % (label, lab, busy, valu, coex, only))
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2])
@@ -219,6 +266,8 @@ if __name__ == "__main__":
     elif sys.argv[1] == "pmcproj":
         pmcproj(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024,
                 sys.argv[5] if len(sys.argv) > 5 else None)
+    elif sys.argv[1] == "sq":
+        sq(sys.argv[2], sys.argv[3], sys.argv[4])
     elif sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 1024)
     else:
