@@ -1424,7 +1424,8 @@ static void launch_gemv_form(const GemmArgs& g, int epi, const GemvShape& sh, hi
 // The small-M kernels serve f16 activations up to 32 rows when K's k-steps
 // divide into whole-depth shares.
 static bool use_gemv(const PackedWeight& w, int xk, int M, int ncu) {
-  return xk == XK_F16 && M <= 32 && gemv_shape(w, EPI_F32, M, ncu).w > 0;
+  return xk == XK_F16 && M <= 32 && w.form != TGOHIP_FORM_F16 &&
+         gemv_shape(w, EPI_F32, M, ncu).w > 0;
 }
 
 // Split-K factor: enough workgroups to cover the chip twice, while each split
