@@ -1,7 +1,7 @@
 """BASELINE config 2 as an op: ragged paged attention over one launch
 (tgohip_paged_attention_replay: the launch planned once, its kernels replayed).
 
-    python -m tgo_amd.attn_bench [--iters 50] [--q f16|f32] [--seed 2]
+    python -m tgo_amd.attn_bench [--iters 50] [--q f16|f32] [--seed 2] [--only decode|prefill]
 
 Config 2: 64 sequences with context lengths uniform in [1, 4096]; 56 decode rows
 (one token each) and 8 prefill chunks of min(256, L) tokens; 32 q / 8 kv heads,
@@ -14,7 +14,8 @@ Algorithmic bytes per launch (HBM-bound): every position a sequence reads, once
 (T * H * d_h * (2 + 2) with f16 q, * (4 + 4) with f32). Flops: 4 * d_h * H per
 visible (query, key) pair. Reported: the median launch time of `iters` replays
 (HIP events around the replay, divided by iters), GB/s against 8 TB/s, TFLOP/s
-against 2.5 PFLOP/s.
+against 2.5 PFLOP/s. --only keeps the 56 decode sequences or the 8 prefill chunks alone
+(the same pages), to see what each part of the launch costs.
 """
 import argparse
 import math
@@ -27,7 +28,7 @@ import tgo_amd
 DH = 128
 
 
-def c2(seed):
+def c2(seed, only=None):
     rng = np.random.default_rng(seed)
     B, H, Hkv, block = 64, 32, 8, 16
     L = rng.integers(1, 4097, size=B)
@@ -42,6 +43,10 @@ def c2(seed):
     for s in range(B):
         pages[s, :need[s]] = perm[at:at + need[s]]
         at += need[s]
+    if only:
+        keep = slice(0, 56) if only == "decode" else slice(56, B)
+        L, ext, pages = L[keep], ext[keep], pages[keep]
+        B = len(L)
     return dict(B=B, H=H, Hkv=Hkv, block=block, L=L, ext=ext, pages=pages, maxp=maxp,
                 T=int(ext.sum()), pool=pool)
 
@@ -51,8 +56,9 @@ def main():
     p.add_argument("--iters", type=int, default=50)
     p.add_argument("--q", default="f16", choices=["f16", "f32"])
     p.add_argument("--seed", type=int, default=2)
+    p.add_argument("--only", default=None, choices=["decode", "prefill"])
     args = p.parse_args()
-    c = c2(args.seed)
+    c = c2(args.seed, args.only)
     H, Hkv, T, block = c["H"], c["Hkv"], c["T"], c["block"]
     positions = c["pool"] * block
     g = torch.Generator(device="cuda").manual_seed(args.seed)
@@ -86,8 +92,8 @@ def main():
                 for L, n in zip(c["L"], c["ext"]))
     flops = 4.0 * DH * H * pairs
     gbps = (kv + qio) / ms / 1e6
-    print("config 2: %d sequences (56 decode rows + 8 chunks, %d rows), sum L = %d, q %s" %
-          (c["B"], T, int(c["L"].sum()), args.q))
+    print("config 2%s: %d sequences (%d rows), sum L = %d, q %s" %
+          (" (%s only)" % args.only if args.only else "", c["B"], T, int(c["L"].sum()), args.q))
     print("bytes/launch %.1f MB (K+V %.1f MB, q in + out %.1f MB); flops/launch %.2f GFLOP" %
           ((kv + qio) / 1e6, kv / 1e6, qio / 1e6, flops / 1e9))
     print("launch %.2f us (median of 5 x %d replays): %.0f GB/s = %.3f of 8 TB/s; %.1f TFLOP/s "
