@@ -1555,13 +1555,18 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
   tiles_n = (nb + 2 * nw - 1) / (2 * nw);
   tiles = tiles_n * rows;
   splits = choose_pipe_splits(tiles, w.K / 64, ncu * (8 / nw));
-  // The exact kernel's workgroups run three times the MFMAs: a launch that
-  // fills half to three quarters of the slots leaves most CUs one workgroup
-  // and the rest a second one, so it splits K to give every CU about two
-  // rounds (the O and down projections at 1152 rows, 288 tiles: 4 splits,
-  // 131 -> 118 and 377 -> 296 us with the standalone reduction).
-  if (ex && splits == 1 && 4 * tiles < 3 * ncu * (8 / nw)) {
-    splits = std::min(4, (2 * ncu * (8 / nw) + tiles - 1) / tiles);
+  // The exact kernel's workgroups run three times the MFMAs, so an unsplit
+  // launch's uneven last round costs more. Under 80% of one round of slots
+  // it leaves most CUs one workgroup and the rest a second one: 4 splits
+  // (the C4 O and down at 1152 rows, 288 tiles: 131 -> 118 and 377 -> 296 us
+  // with the standalone reduction; the C5 O and down at 1280 rows, 400 tiles:
+  // 342 -> 296 and 1011 -> 889 us in the step). One to 1.6 rounds: 2 splits
+  // (the C5 QKV, 800 tiles: 404 -> 372 us). The C4 QKV (432 tiles, 84% of a
+  // round) gained nothing from 2-5 splits and stays whole.
+  if (ex && splits == 1) {
+    const int slots = ncu * (8 / nw);
+    if (5 * tiles < 4 * slots) splits = 4;
+    else if (tiles > slots && 5 * tiles < 8 * slots) splits = 2;
     while (splits > 1 && (w.K / 64) / splits < 8) splits--;
   }
   if (ex && pipe_ex_splits() > 0) {

@@ -1309,7 +1309,8 @@ int tgohip_linear_noalloc(tgohip_ctx* c, int handle, const void* x, int x_dtype,
   if (!w) return TGOHIP_EINVAL;
   if (M < 0) return fail(TGOHIP_EINVAL, "linear_noalloc: M is " + std::to_string(M));
   if (M == 0) return 0;  // an empty batch: nothing to launch
-  const size_t ws = gemm_workspace_bytes(*w, M, c->ncu);
+  // exactly what this call's kernels use (its activation type decides them)
+  const size_t ws = gemm_workspace_bytes(*w, M, c->ncu, xkind(x_dtype));
   if (ws > kScratchBytes)
     return fail(TGOHIP_EINVAL, "linear_noalloc: M = " + std::to_string(M) + " over [" +
                                    std::to_string(w->K) + "," + std::to_string(w->N) +
