@@ -248,8 +248,8 @@ int tgohip_linear(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M
 int tgohip_linear_noalloc(tgohip_ctx* ctx, int handle, const void* x, int x_dtype, int M,
                           void* y, int y_dtype);
 /* Bytes of split-K partials a linear call over M rows of a handle's weight
- * with f16 (x_dtype TGOHIP_F16) or f32 activations needs: 0 when it runs
- * unsplit. tgohip_linear_noalloc refuses calls above 64 MiB. */
+ * with activations of x_dtype (TGOHIP_F16, TGOHIP_F32 or TGOHIP_F16X2) needs:
+ * 0 when it runs unsplit. tgohip_linear_noalloc refuses calls above 64 MiB. */
 int tgohip_linear_workspace(tgohip_ctx* ctx, int handle, int x_dtype, int M, size_t* bytes);
 
 /* Dequantizes a handle's weight to f32 [K,N] on the device exactly as the
