@@ -125,6 +125,16 @@ int tgohip_get_config(tgohip_ctx* ctx, tgohip_model_cfg* cfg);
  * F16 or I8 (QuantGatherRows, model/qwen3_graph.go:57-61). */
 int tgohip_weight(tgohip_ctx* ctx, const char* port, int form, int K, int N,
                   const void* plane, const void* scales, const void* zeros);
+/* tgohip_weight from an f32 plane, quantized on the device: weights.Load's
+ * quantize-then-upload of a projection or of the int8-capped embedding
+ * (weights/weights.go:694-743; quantizeInto, weights/convert.go:206-217).
+ * w: host [K,N] f32 (already transposed and q/k-permuted); form I8 or I4_TGO.
+ * The device codes, scales and zeros equal tgohip_quantize_int8 /
+ * tgohip_quantize_int4's on the same plane, bit for bit (NaN, infinities and
+ * values past f16's range included), so the result is that of those calls
+ * followed by tgohip_weight; the quantization runs at device speed instead of
+ * one f64 division per element on the host. */
+int tgohip_weight_f32(tgohip_ctx* ctx, const char* port, int form, int K, int N, const float* w);
 /* Uploads an f32 norm gain (nn/nn.go:266-274, gains.go:40-69):
  * "<l>.attn_norm|ffn_norm" [d], "<l>.qnorm|knorm" [d_h], "final_norm" [d]. */
 int tgohip_gain(tgohip_ctx* ctx, const char* port, const float* g, int width);
@@ -222,6 +232,9 @@ int tgohip_greedy(tgohip_ctx* ctx, const float* logits, int B, int V, int32_t* i
 /* Uploads a weight for tgohip_linear under a handle (any form above). */
 int tgohip_weight_upload(tgohip_ctx* ctx, int form, int K, int N, const void* plane,
                          const void* scales, const void* zeros, int* handle);
+/* tgohip_weight_upload from an f32 [K,N] host plane quantized on the device
+ * (I8 or I4_TGO), as tgohip_weight_f32 does for a port. */
+int tgohip_weight_upload_f32(tgohip_ctx* ctx, int form, int K, int N, const float* w, int* handle);
 /* Synthesises a [K,N] weight of `form` on the device under a handle, from
  * (seed, stream) as tgohip_synth_weights does for a port. */
 int tgohip_weight_synth(tgohip_ctx* ctx, int form, int K, int N, uint64_t seed, uint64_t stream,

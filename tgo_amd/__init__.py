@@ -73,6 +73,8 @@ def lib():
         "tgohip_use_own_stream": (I, [P]),
         "tgohip_config": (I, [P, ctypes.POINTER(ModelCfg)]),
         "tgohip_weight": (I, [P, ctypes.c_char_p, I, I, I, P, P, P]),
+        "tgohip_weight_f32": (I, [P, ctypes.c_char_p, I, I, I, P]),
+        "tgohip_weight_upload_f32": (I, [P, I, I, I, P, P]),
         "tgohip_gain": (I, [P, ctypes.c_char_p, P, I]),
         "tgohip_synth_weights": (I, [P, U64, I, D]),
         "tgohip_kv_alloc": (I, [P, I]),
@@ -470,6 +472,12 @@ class Context:
         check(lib().tgohip_weight(self.h, port.encode(), form, K, N, ptr(plane), ptr(scales),
                                   ptr(zeros)))
 
+    def weight_f32(self, port, form, K, N, w):
+        """tgohip_weight from an f32 [K,N] plane, quantized (I8, I4_TGO) on the device."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        assert w.size == K * N
+        check(lib().tgohip_weight_f32(self.h, port.encode(), form, K, N, ptr(w)))
+
     def gain(self, port, g):
         g = np.ascontiguousarray(g, dtype=np.float32)
         check(lib().tgohip_gain(self.h, port.encode(), ptr(g), g.size))
@@ -561,6 +569,14 @@ class Context:
         h = ctypes.c_int()
         check(lib().tgohip_weight_upload(self.h, form, K, N, ptr(plane), ptr(scales), ptr(zeros),
                                          ctypes.byref(h)))
+        return h.value
+
+    def weight_upload_f32(self, form, K, N, w):
+        """An op-level weight from an f32 [K,N] plane quantized (I8, I4_TGO) on the device."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        assert w.size == K * N
+        h = ctypes.c_int()
+        check(lib().tgohip_weight_upload_f32(self.h, form, K, N, ptr(w), ctypes.byref(h)))
         return h.value
 
     def weight_synth(self, form, K, N, seed, stream, sigma):

@@ -219,6 +219,10 @@ void launch_synth_i4sym(uint64_t seed, uint64_t stream, int K, int N, uint32_t* 
 void launch_synth_i4tgo(uint64_t seed, uint64_t stream, size_t n, uint32_t* out, hipStream_t st);
 void launch_synth_zero(uint64_t seed, uint64_t stream, size_t n, uint16_t* out, hipStream_t st);
 void launch_synth_i8(uint64_t seed, uint64_t stream, size_t n, int8_t* out, hipStream_t st);
+// load-time quantizers (the host's tgohip_quantize_int8 / _int4, bit for bit)
+void launch_quantize_i8(const float* w, size_t n, int8_t* q, uint16_t* scales, hipStream_t st);
+void launch_quantize_i4tgo(const float* w, size_t n, uint32_t* codes, uint16_t* scales,
+                           uint16_t* zeros, hipStream_t st);
 void launch_synth_gain(uint64_t seed, uint64_t stream, size_t n, float* out, hipStream_t st);
 void launch_fill_f32(float* p, size_t n, float v, hipStream_t st);
 

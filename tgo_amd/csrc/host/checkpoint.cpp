@@ -811,18 +811,8 @@ static int load_projection(tgohip_ctx* ctx, const Spec& s, const std::vector<flo
     if (saturated) *saturated += (int64_t)sat;
     return tgohip_weight(ctx, s.port.c_str(), form, (int)K, (int)N, h.data(), nullptr, nullptr);
   }
-  if (form == TGOHIP_FORM_I8) {
-    std::vector<int8_t> q(n);
-    std::vector<uint16_t> sc((n + 31) / 32);
-    tgohip_quantize_int8(p.data(), n, q.data(), sc.data());
-    return tgohip_weight(ctx, s.port.c_str(), form, (int)K, (int)N, q.data(), sc.data(), nullptr);
-  }
-  if (form == TGOHIP_FORM_I4_TGO) {
-    std::vector<uint32_t> codes((n + 7) / 8);
-    std::vector<uint16_t> sc((n + 127) / 128), zr((n + 127) / 128);
-    tgohip_quantize_int4(p.data(), n, codes.data(), sc.data(), zr.data());
-    return tgohip_weight(ctx, s.port.c_str(), form, (int)K, (int)N, codes.data(), sc.data(), zr.data());
-  }
+  if (form == TGOHIP_FORM_I8 || form == TGOHIP_FORM_I4_TGO)  // quantized on the device
+    return tgohip_weight_f32(ctx, s.port.c_str(), form, (int)K, (int)N, p.data());
   return fail(TGOHIP_EINVAL, "weights: load form " + std::to_string(form) +
                                  " is not F16, I8 or the int4 pack tgo stores (I4_TGO)");
 }

@@ -483,6 +483,86 @@ __device__ __forceinline__ uint16_t f16_loader_bits(float x) {
   return (uint16_t)(sign | (uint16_t)(((uint32_t)(e + 15) << 10) + keep));
 }
 
+// ---- load-time quantizers on the device ------------------------------------
+// The host's tgohip_quantize_int8 (quantizeInto, weights/convert.go:206-217)
+// and tgohip_quantize_int4 (the int4 triple of weights/weights.go:694-743)
+// restated so that a checkpoint's f32 planes quantize where they are uploaded,
+// with the same bits: the same f32 and f64 operations in the same order (IEEE
+// division, round-half-even), the loader's f16 rule (f16_loader_bits), and
+// std::min / std::max's comparisons, so a
+// NaN is skipped or clamped exactly as on the host. One thread per group, its
+// elements in order.
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(half_t, h);  // the rule's outputs: normal, zero, +-65504, NaN
+}
+
+__global__ void quantize_i8_kernel(const float* w, size_t n, int8_t* q, uint16_t* scales) {
+  const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x, lo = g * 32;
+  if (lo >= n) return;
+  const size_t hi = lo + 32 < n ? lo + 32 : n;
+  float peak = 0.f;
+  for (size_t i = lo; i < hi; i++) {
+    const float a = fabsf(w[i]);
+    peak = (peak < a) ? a : peak;  // std::max(peak, a)
+  }
+  const uint16_t s16 = f16_loader_bits(peak / 127.0f);
+  const float s = f16_bits_to_f32(s16);
+  scales[g] = s16;
+  for (size_t i = lo; i < hi; i++) {
+    double v = s > 0 ? rint((double)w[i] / (double)s) : 0.0;
+    v = (v < 127.0) ? v : 127.0;    // std::min(127.0, v)
+    v = (-127.0 < v) ? v : -127.0;  // std::max(-127.0, v)
+    q[i] = (int8_t)v;
+  }
+}
+
+__global__ void quantize_i4tgo_kernel(const float* w, size_t n, uint32_t* codes, uint16_t* scales,
+                                      uint16_t* zeros) {
+  const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x, lo = g * 128;
+  if (lo >= n) return;
+  const size_t hi = lo + 128 < n ? lo + 128 : n;
+  float mn = w[lo], mx = w[lo];
+  for (size_t i = lo; i < hi; i++) {
+    const float x = w[i];
+    mn = (x < mn) ? x : mn;  // std::min(mn, x)
+    mx = (mx < x) ? x : mx;  // std::max(mx, x)
+  }
+  const float sr = (mx - mn) / 15.0f;
+  uint16_t s16 = f16_loader_bits(sr > 0 ? sr : 1.0f);
+  float s = f16_bits_to_f32(s16);
+  if (s == 0) {
+    s16 = 0x3c00;
+    s = 1.0f;
+  }
+  double zf = rint(-(double)mn / (double)s);
+  zf = (zf < 15.0) ? zf : 15.0;  // std::min(15.0, zf)
+  zf = (0.0 < zf) ? zf : 0.0;    // std::max(0.0, zf)
+  scales[g] = s16;
+  zeros[g] = f16_loader_bits((float)zf);
+  for (size_t i0 = lo; i0 < hi; i0 += 8) {
+    uint32_t word = 0;
+    for (size_t i = i0; i < i0 + 8 && i < hi; i++) {
+      double v = rint((double)w[i] / (double)s + zf);
+      v = (v < 15.0) ? v : 15.0;
+      v = (0.0 < v) ? v : 0.0;
+      word |= ((uint32_t)v & 15u) << (4 * (i % 8));
+    }
+    codes[i0 / 8] = word;
+  }
+}
+
+void launch_quantize_i8(const float* w, size_t n, int8_t* q, uint16_t* scales, hipStream_t st) {
+  const size_t groups = (n + 31) / 32;
+  hipLaunchKernelGGL(quantize_i8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, w, n,
+                     q, scales);
+}
+void launch_quantize_i4tgo(const float* w, size_t n, uint32_t* codes, uint16_t* scales,
+                           uint16_t* zeros, hipStream_t st) {
+  const size_t groups = (n + 127) / 128;
+  hipLaunchKernelGGL(quantize_i4tgo_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st,
+                     w, n, codes, scales, zeros);
+}
+
 // F16 plane: loader-rule f16 of f32(N(0,1) * sigma).
 __global__ void synth_f16_kernel(uint64_t seed, uint64_t stream, size_t n, double sigma,
                                  uint16_t* out) {

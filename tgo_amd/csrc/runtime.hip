@@ -310,6 +310,34 @@ int canon_alloc(Canon& cn, int form, int K, int N) {
   return 0;
 }
 
+struct DevFree {
+  void* p;
+  ~DevFree() { (void)hipFree(p); }
+};
+
+// The canonical form of an f32 host plane, quantized on the device (I8 or
+// I4_TGO) into cn: the codes of tgohip_quantize_int8 / _int4, bit for bit.
+int canon_quantize(tgohip_ctx* c, Canon& cn, int form, int K, int N, const float* w) {
+  if (form != TGOHIP_FORM_I8 && form != TGOHIP_FORM_I4_TGO)
+    return fail(TGOHIP_EINVAL, "weight_f32: the device quantizes to I8 or I4_TGO (form " +
+                                   std::to_string(form) + "); f16 converts on the host (tgohip_to_f16)");
+  if (!w) return fail(TGOHIP_EINVAL, "weight: the plane is missing");
+  int rc = canon_alloc(cn, form, K, N);
+  if (rc) return rc;
+  const size_t n = (size_t)K * N;
+  float* dw = nullptr;
+  TGOHIP_HIP(hipMalloc((void**)&dw, n * sizeof(float)));
+  DevFree hold{dw};
+  TGOHIP_HIP(hipMemcpyAsync(dw, w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  if (form == TGOHIP_FORM_I8)
+    launch_quantize_i8(dw, n, (int8_t*)cn.plane, cn.scales, c->stream);
+  else
+    launch_quantize_i4tgo(dw, n, (uint32_t*)cn.plane, cn.scales, cn.zeros, c->stream);
+  TGOHIP_HIP(hipGetLastError());
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));  // the staging plane is freed on return
+  return 0;
+}
+
 int canon_upload(tgohip_ctx* c, Canon& cn, int form, int K, int N, const void* plane,
                  const void* scales, const void* zeros) {
   int rc = canon_alloc(cn, form, K, N);
@@ -660,6 +688,51 @@ int tgohip_weight(tgohip_ctx* c, const char* port, int form, int K, int N, const
   if (rc) return rc;
   rc = place_weight(c, kind, l, form, K, N, cn, port);
   if (rc) return rc;
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+// An f32 plane quantized on the device: the canonical codes of
+// tgohip_quantize_int8 / tgohip_quantize_int4 (bit for bit), then placed as
+// tgohip_weight places them.
+int tgohip_weight_f32(tgohip_ctx* c, const char* port, int form, int K, int N, const float* w) {
+  if (!c->configured) return fail(TGOHIP_ESTATE, "weight: configure the context first");
+  int l;
+  const PortKind kind = parse_port(port, l);
+  if (kind == P_BAD || (l >= 0 && l >= c->cfg.layers))
+    return fail(TGOHIP_EINVAL, std::string("weight: no port named ") + port);
+  if (kind == P_EMBED) {
+    if (form != TGOHIP_FORM_I8)
+      return fail(TGOHIP_EINVAL, "weight_f32 embed: the device quantizes the gathered embedding to "
+                                 "int8 (weights/weights.go:543-545 caps int4 to int8; f16 converts "
+                                 "on the host)");
+    if (K != c->cfg.vocab || N != c->cfg.hidden)
+      return fail(TGOHIP_EINVAL, "weight embed is [" + std::to_string(K) + "," + std::to_string(N) +
+                                     "] and the config asks for [vocab, hidden]");
+    if (!w) return fail(TGOHIP_EINVAL, "weight: the plane is missing");
+    const size_t n = (size_t)K * N;
+    float* dw = nullptr;
+    TGOHIP_HIP(hipMalloc((void**)&dw, n * sizeof(float)));
+    DevFree hold{dw};
+    TGOHIP_HIP(hipMemcpyAsync(dw, w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    free_owned(c, c->embed);
+    free_owned(c, c->embed_scales);
+    c->embed_scales = nullptr;
+    int rc = alloc_owned(c, &c->embed, plane_bytes(form, K, N));
+    if (rc) return rc;
+    rc = alloc_owned(c, (void**)&c->embed_scales, scale_count(form, K, N) * 2);
+    if (rc) return rc;
+    launch_quantize_i8(dw, n, (int8_t*)c->embed, (uint16_t*)c->embed_scales, c->stream);
+    TGOHIP_HIP(hipGetLastError());
+    TGOHIP_HIP(hipStreamSynchronize(c->stream));
+    c->embed_form = form;
+    return 0;
+  }
+  int rc = check_shape(form, K, N, port);
+  if (rc) return rc;
+  Canon cn;
+  if ((rc = canon_quantize(c, cn, form, K, N, w))) return rc;
+  if ((rc = place_weight(c, kind, l, form, K, N, cn, port))) return rc;
   TGOHIP_HIP(hipStreamSynchronize(c->stream));
   return 0;
 }
@@ -1245,6 +1318,21 @@ int tgohip_weight_upload(tgohip_ctx* c, int form, int K, int N, const void* plan
   TGOHIP_HIP(hipStreamSynchronize(c->stream));
   *handle = c->next_handle++;
   c->handles[*handle] = w;
+  return 0;
+}
+
+// tgohip_weight_upload from an f32 plane quantized on the device.
+int tgohip_weight_upload_f32(tgohip_ctx* c, int form, int K, int N, const float* w, int* handle) {
+  int rc = check_shape(form, K, N, "weight");
+  if (rc) return rc;
+  Canon cn;
+  if ((rc = canon_quantize(c, cn, form, K, N, w))) return rc;
+  PackedWeight pw;
+  if ((rc = alloc_packed(c, pw, form, K, N))) return rc;
+  if ((rc = repack_enqueue(form, cn.plane, cn.scales, cn.zeros, K, N, pw, 1, 0, c->stream))) return rc;
+  TGOHIP_HIP(hipStreamSynchronize(c->stream));
+  *handle = c->next_handle++;
+  c->handles[*handle] = pw;
   return 0;
 }
 
