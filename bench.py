@@ -722,7 +722,10 @@ def main():
     # the committed counters were taken at the default arithmetic and weight form only
     gu_traffic = recorded_proj_traffic("mixed", "gateup") \
         if args.precision == 1 and args.form == tgo_amd.FORM_I4_SYM else None
-    mfma_per_product = 3 if args.precision == 1 else 1
+    # tgo's arithmetic: symmetric int4 factors its group scale out (activation
+    # hi.code + lo.code, the scale applied in f32); the other forms multiply
+    # the exact dequantized weight's hi and lo parts (hi.hi + lo.hi + hi.lo)
+    mfma_per_product = 1 if args.precision == 0 else (2 if args.form == 3 else 3)
     rows_per_step = (total_pf + total_dc) / args.steps
     result = {
         "metric": "output tok/s, Qwen3-8B int4 ragged batch, 1 MI355X; paged-attn HBM GB/s",
@@ -735,7 +738,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if args.precision == 0 else "f32 (f16 hi+lo operand pairs, 3 MFMAs per product)",
+        "dtype": "f16" if args.precision == 0 else (
+            "f32 (f16 hi+lo activation pairs times the exact int4 codes, 2 MFMAs per product, "
+            "group scale applied in f32)" if args.form == 3 else
+            "f32 (f16 hi+lo operand pairs, 3 MFMAs per product)"),
         "data": "synthetic (seeded random-init int4 weights, seeded token ids, synthetic KV for "
                 "the initial contexts)",
         "config": {
@@ -766,9 +772,11 @@ def main():
             "algorithmic_bytes_per_launch": round(gu_bytes / max(gu_n, 1)),
             "flops_per_launch": round(gu_flops / max(gu_n, 1)),
             "flops_counted": "algorithmic, 2*M*K*N; the kernel executes %d f16 MFMAs per "
-                             "product (%s)" % (mfma_per_product,
-                                               "activation hi.weight hi + lo.hi + hi.lo"
-                                               if mfma_per_product == 3 else "f16 operands"),
+                             "product (%s)" % (mfma_per_product, {
+                                 3: "activation hi.weight hi + lo.hi + hi.lo",
+                                 2: "activation hi.code + lo.code into a per-group sum, "
+                                    "times the group's scale in f32",
+                                 1: "f16 operands"}[mfma_per_product]),
             "executed_mfma_frac": round(mfma_per_product * gu_tflops / MFMA_F16_PEAK, 4),
             "avg_launch_ms": round(avg_gu_ms, 4),
             "launches": gu_n,

@@ -126,6 +126,44 @@ def test_linear_matches_the_oracle(ctx, torch_gpu, form, M, xk):
     assert np.all(np.abs(got - cpu) <= tol2), np.max(np.abs(got - cpu) / tol2)
 
 
+@pytest.mark.parametrize("K", [512, 2048])
+@pytest.mark.parametrize("M", [64, 200])
+def test_exact_int4_sym_scales_across_the_f16_range(ctx, torch_gpu, K, M):
+    """Symmetric int4 in tgo's arithmetic (activation pairs, the pipelined exact kernel:
+    K = 512 one unsplit launch with two k groups per workgroup, K = 2048 split-K) with
+    group scales planted across f16's whole range: the largest finite (65504, so
+    |q s| reaches 524032, past f16), large, ordinary, the smallest normal and
+    subnormal. The kernel multiplies the exact codes and applies each group's scale in
+    f32, so every product stays the f32 dequantized weight's; against the f64 product
+    of the f32 activations and the oracle's dequantization, AccumF32 + 2^-22."""
+    torch = torch_gpu
+    import tgo_amd
+    N = 256
+    qw, sc = oracle.synth_int4_sym(11, 4, K, N, 0.02)
+    planted = np.array([65504.0, 60000.0, 1000.0, 1.0, 0.01, 2.0 ** -14, 2.0 ** -20, 2.0 ** -24],
+                       np.float16).view(np.uint16)
+    g = np.arange(K // 32)[:, None] + 3 * np.arange(N)[None, :]
+    sc = np.ascontiguousarray(planted[g % len(planted)])
+    w64 = oracle.dequant(3, K, N, qw, sc).astype(np.float64)
+    assert np.isfinite(w64).all() and np.abs(w64).max() > 65504
+    rng = np.random.default_rng(K + M)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    hi, lo = split_pair(x)
+    h = ctx.weight_upload(3, K, N, qw, sc)
+    try:
+        dx = torch.from_numpy(np.concatenate([hi.ravel(), lo.ravel()])).cuda()
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.linear(h, dx, M, y, x_dtype=tgo_amd.F16X2)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().astype(np.float64)
+    finally:
+        ctx.weight_free(h)
+    xu = x.astype(np.float64)
+    ref = xu @ w64
+    tol = (4 * np.sqrt(K) * 2.0 ** -24 + 2.0 ** -22) * (np.abs(xu) @ np.abs(w64))
+    assert np.all(np.abs(got - ref) <= tol), np.max(np.abs(got - ref) / tol)
+
+
 def test_linear_is_deterministic_and_row_independent(ctx, torch_gpu):
     """A row's result does not depend on the rows beside it when the tile
     configuration is the same (M in one tile class)."""

@@ -77,6 +77,23 @@ __device__ __forceinline__ half8_t deq_i4_sym(uint32_t w, half_t s) {
   }
   return o;
 }
+// The codes q - 8 of one substep's B fragment, unscaled: small integers, exact
+// in f16 (the masks and merge constants of deq_i4_sym).
+__device__ __forceinline__ half8_t i4_sym_codes(uint32_t w) {
+  uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, g0 = 0x64006400u, g1 = 0x54005400u;
+  asm("" : "+v"(m0), "+v"(m1), "+v"(g0), "+v"(g1));
+  const half2_t b0 = {(half_t)1032.f, (half_t)1032.f}, b1 = {(half_t)72.f, (half_t)72.f};
+  const uint32_t w8 = w >> 8;
+  const half2_t h[4] = {as_h2((w & m0) | g0) - b0, as_h2((w & m1) | g1) - b1,
+                        as_h2((w8 & m0) | g0) - b0, as_h2((w8 & m1) | g1) - b1};
+  half8_t o;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    o[2 * j] = h[j][0];
+    o[2 * j + 1] = h[j][1];
+  }
+  return o;
+}
 __device__ __forceinline__ half8_t deq_i4_asym(uint32_t w, half8_t s, half8_t zz) {
   half8_t o;
 #pragma unroll
@@ -604,10 +621,18 @@ __device__ __forceinline__ void pipe_bfrag_x(const PipeB<TGOHIP_FORM_I8>& r, int
 // pair, hi and lo planes DMA'd side by side into each stage, and the weights
 // the exact hi + lo pair (pipe_bfrag_x): three MFMAs per product (hi.hi,
 // lo.hi, hi.lo), the f32 activation times the unrounded dequantized weight.
+// Symmetric int4 (one scale per 32 k of a column) factors instead:
+// sum_k x w = sum_g s_g (sum_{k in g} x q), and the codes q are exact f16, so
+// each group's inner sum is two MFMAs (x_hi.q, x_lo.q) into a group
+// accumulator that one f32 fma per output then scales into the sum. Every
+// product x_hi q, x_lo q is exact and s_g multiplies in f32, so this is
+// tgo's f32 dequantize-then-dot up to f32 rounding order, with the lo.lo term
+// (2^-22 relative) dropped as in the three-MFMA form.
 template <int FORM, int EPI, int MW, int NW, int KQ = 1, bool EX = false>
 __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_kernel(
     GemmArgs g, int tiles_n, int tiles, int colmajor, int xsplit) {
   constexpr int MB = MW / 32;
+  constexpr bool FX = EX && FORM == TGOHIP_FORM_I4_SYM;  // factored scales
   constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step and plane
   constexpr int AP = EX ? 2 : 1;      // activation planes per stage
   static_assert(KQ == 1 || (KQ == 2 && NW * MW * 256 <= 4 * 2 * MW * 128),
@@ -723,6 +748,8 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
     for (int b = 0; b < 2; b++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mb][b][r] = 0.f;
+  float16_t accg[FX ? MB : 1][2];  // FX: the current scale group's inner sums
+  const float16_t zero16 = {};
 
   // A(k) (and the scales of B(k) when they travel by LDS) sits in LDS stage
   // k % 4, DMA'd in the middle of step k-3; B(k) in register slot k % 4,
@@ -753,7 +780,8 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
                     half8_t (&bl)[2]) {
 #pragma unroll
     for (int b = 0; b < 2; b++) {
-      if constexpr (EX) pipe_bfrag_x(bb[b], j, sz, b, h, bh[b], bl[b]);
+      if constexpr (FX) bh[b] = i4_sym_codes(word_of(bb[b].p, j));
+      else if constexpr (EX) pipe_bfrag_x(bb[b], j, sz, b, h, bh[b], bl[b]);
       else bh[b] = pipe_bfrag(bb[b], j, sz, b, h);
     }
   };
@@ -801,12 +829,43 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
           read_a(An, h, afn, afnl);
           read_b(bq[(u + 1) % 4], 0, Sz[(u + 1) % 4] + sq + wave * 256, bfn, bfnl);
         }
+        if constexpr (FX) {
+          // substeps 0-1 are the k-step's first scale group, 2-3 its second;
+          // an even substep starts the group's sums, an odd one ends them
+          // and scales them into acc
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++)
+          for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-          for (int b = 0; b < 2; b++)
-            acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
-        if constexpr (EX) {
+            for (int b = 0; b < 2; b++)
+              accg[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                  afc[mb], bfc[b], (j & 1) ? accg[mb][b] : zero16, 0, 0, 0);
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+              accg[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afcl[mb], bfc[b], accg[mb][b], 0, 0, 0);
+          if (j & 1) {
+            // the lane's column scale of this group (bq[u] holds step u's
+            // two scales per lane column)
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+              union { uint32_t u; half2_t h; } sc;
+              sc.u = bq[u][b].s;
+              const float s = (float)sc.h[j >> 1];
+#pragma unroll
+              for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[mb][b][r] = __builtin_fmaf(accg[mb][b][r], s, acc[mb][b][r]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfc[b], acc[mb][b], 0, 0, 0);
+        }
+        if constexpr (EX && !FX) {
           // the two correction products, each pass over every block, so no
           // MFMA waits on the one just issued into the same accumulator
 #pragma unroll
@@ -820,7 +879,20 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
             for (int b = 0; b < 2; b++)
               acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfcl[b], acc[mb][b], 0, 0, 0);
         }
-        if constexpr (EX) {
+        if constexpr (FX) {
+          // 8 MFMAs (64-row tiles), 4 LDS reads, the codes' 18 VALU; an odd
+          // substep adds the 64 scaling fmas
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            if (j & 1) __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
+            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if (j & 1) __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
+            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          }
+        } else if constexpr (EX) {
           // 12 MFMAs (64-row tiles), 4 LDS reads, the B pairs' 36 VALU
 #pragma unroll
           for (int q = 0; q < 4; q++) {
