@@ -83,13 +83,15 @@ int tgohip_set_stream(tgohip_ctx* ctx, void* stream);
 int tgohip_use_own_stream(tgohip_ctx* ctx);
 /* Arithmetic of the step. 1 (the default) is tgo's CPU path (nn/blocks.go:13-21): every
  * projection multiplies the f32 activation (carried as an f16 high + low pair,
- * ~22 bits) by the unrounded dequantized weight (carried as an exact f16
- * high + low pair), f32 accumulate -- three f16 MFMAs per product -- and
- * attention weights V by the f32 softmax probabilities (hi + lo); logits stay
- * within 2e-3 of tgo's CPU path through every layer of the 8B and 32B shapes.
- * 0 rounds activations, weights and probabilities to f16 for one MFMA each:
- * about 2.4x faster, with an f16 storage error per operand that grows with
- * depth (about 5e-3 of the row's largest logit after 36 layers). */
+ * ~22 bits) by the unrounded dequantized weight, f32 accumulate: symmetric
+ * int4 as the exact codes with each 32-k group's scale applied in f32 (two
+ * f16 MFMAs per product), the other forms as an exact f16 high + low weight
+ * pair (three) -- and attention weights V by the f32 softmax probabilities
+ * (hi + lo); logits stay within 2e-3 of tgo's CPU path through every layer of
+ * the 8B and 32B shapes. 0 rounds activations, weights and probabilities to
+ * f16 for one MFMA each: 1.6-2.2x faster, with an f16 storage error per
+ * operand that grows with depth (about 5e-3 of the row's largest logit after
+ * 36 layers). */
 int tgohip_set_precision(tgohip_ctx* ctx, int mode);
 /* Prefix-shared (cascade) attention, the "read a shared page once" design of
  * tgo's prefix cache (internal/prefix block sharing; specs/016-prefix-cache.md).
