@@ -845,8 +845,18 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
             for (int b = 0; b < 2; b++)
               accg[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afcl[mb], bfc[b], accg[mb][b], 0, 0, 0);
           if (j & 1) {
-            // the lane's column scale of this group (bq[u] holds step u's
-            // two scales per lane column)
+            // The scaling reads the group's last MFMAs, so this wave has no
+            // MFMA to issue beside it: at the lower priority the other wave
+            // on the SIMD issues first (the C4 step 40.1-40.5 -> 39.1 ms;
+            // gate/up 407 -> 390-399 us, QKV 116 -> 106-111 us). With two k
+            // groups per workgroup the isolated block spilled more (18
+            // VGPRs, not 8-11), so they keep the interleave below. The
+            // lane's column scale of this group: bq[u] holds step u's two
+            // per lane column.
+            if constexpr (KQ == 1) {
+              __builtin_amdgcn_sched_barrier(0);
+              __builtin_amdgcn_s_setprio(0);
+            }
 #pragma unroll
             for (int b = 0; b < 2; b++) {
               union { uint32_t u; half2_t h; } sc;
@@ -856,6 +866,10 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
               for (int mb = 0; mb < MB; mb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[mb][b][r] = __builtin_fmaf(accg[mb][b][r], s, acc[mb][b][r]);
+            }
+            if constexpr (KQ == 1) {
+              __builtin_amdgcn_s_setprio(1);
+              __builtin_amdgcn_sched_barrier(0);
             }
           }
         } else {
@@ -880,18 +894,27 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
               acc[mb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[mb], bfcl[b], acc[mb][b], 0, 0, 0);
         }
         if constexpr (FX) {
-          // 8 MFMAs (64-row tiles), 4 LDS reads, the codes' 18 VALU; an odd
-          // substep adds the 64 scaling fmas
+          // 8 MFMAs (64-row tiles), 4 LDS reads, the codes' 18 VALU; with
+          // two k groups an odd substep's 64 scaling fmas fill its VALU
+          // slots (with one, its MFMA region is scheduled freely, above)
+          if ((j & 1) == 0)
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            if (j & 1) __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
-            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            if (j & 1) __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
-            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-          }
+            for (int q = 0; q < 4; q++) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+            }
+          else if (KQ == 2)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+              __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
+            }
         } else if constexpr (EX) {
           // 12 MFMAs (64-row tiles), 4 LDS reads, the B pairs' 36 VALU
 #pragma unroll
