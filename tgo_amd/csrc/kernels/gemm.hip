@@ -1668,7 +1668,12 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
     splits = pipe_ex_splits();
     while (splits > 1 && (w.K / 64) / splits < 8) splits--;
   }
-  if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) && tiles >= ncu / 2)
+  // A SwiGLU launch over half the CUs or more stays whole (the reduction
+  // would apply the epilogue), except an exact one under 80% of a round: the
+  // C4 gate/up at 128 rows (192 tiles, two k groups on 192 of 256 CUs) takes
+  // 4 splits and the reduction, 74 -> 64.5 us with it.
+  if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) && tiles >= ncu / 2 &&
+      !(ex && 5 * tiles < 4 * ncu * (8 / nw)))
     splits = 1;
 }
 
