@@ -138,7 +138,7 @@ struct AttnDevPlan {
 };
 int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
                     const uint32_t* pages, int max_pages, int block, int capacity, int H,
-                    int Hkv, AttnPlan& plan, int cascade_min = 0);
+                    int Hkv, AttnPlan& plan, int cascade_min = 0, bool f32_q = false);
 // out_form: OUT_F32, OUT_F16 or OUT_X2 (lo plane T * H * 128 elements after hi).
 int attn_enqueue(const AttnPlan& plan, const AttnDevPlan& dp, const void* q, int q_f16,
                  const void* k, const void* v, void* out, int out_form, int T, int H, int Hkv,

@@ -794,7 +794,7 @@ __global__ void zero_rows_kernel(void* out, int f16, size_t start, size_t count,
 // position a claimed row reads has a page-table entry inside the pool.
 int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* extents,
                     const uint32_t* pages, int max_pages, int block, int capacity, int H,
-                    int Hkv, AttnPlan& plan, int cascade_min) {
+                    int Hkv, AttnPlan& plan, int cascade_min, bool f32_q) {
   if (H <= 0 || Hkv <= 0 || H % Hkv != 0)
     return fail(TGOHIP_EINVAL, "attention: query heads " + std::to_string(H) +
                                    " are not a multiple of kv heads " + std::to_string(Hkv));
@@ -1033,15 +1033,18 @@ int attn_build_plan(int T, int B, const uint32_t* lengths, const uint32_t* exten
       return (x.kv_hi - x.kv_lo) > (y.kv_hi - y.kv_lo);
     };
     std::stable_sort(dec.begin(), dec.end(), heavy);
-    // Decode items go heavy-first, which keeps the tail short. TGOHIP_ATTN_ORDER
-    // = 1 instead takes decode groups (the kv heads of one part) alternately
-    // from the long and the short end beside prefill items, so the prefill
-    // items' MFMA work meets a steady mix of streams: with ordinary K/V loads
-    // that was 2% faster on the C4 step (0.199-0.201 against 0.208-0.218 ms
-    // per launch); with the non-temporal decode loads heavy-first is 0.5%
-    // faster (5218-5283 against 5186-5228 tok/s, five alternating pairs of 60
-    // steps; launch 0.178-0.185 against 0.184-0.189 ms).
-    static const int order = [] { const char* e = getenv("TGOHIP_ATTN_ORDER"); return e ? atoi(e) : 0; }();
+    // Decode items go heavy-first, which keeps the tail short, with f16 q.
+    // With f32 q (tgo's arithmetic: two MFMAs per prefill product) decode
+    // groups (the kv heads of one part) are taken alternately from the long
+    // and the short end beside prefill items, so the heavier prefill MFMA
+    // work meets a steady mix of streams: the C4 launch 0.218-0.220 ->
+    // 0.209-0.212 ms (two alternating pairs of 40 steps). With f16 q and the
+    // non-temporal decode loads heavy-first was 0.5% faster (5218-5283
+    // against 5186-5228 tok/s, five alternating pairs of 60 steps).
+    // TGOHIP_ATTN_ORDER (0 heavy-first, 1 alternating) overrides. The order
+    // changes when items run, not what they compute.
+    static const int order_env = [] { const char* e = getenv("TGOHIP_ATTN_ORDER"); return e ? atoi(e) : -1; }();
+    const int order = order_env >= 0 ? order_env : (f32_q ? 1 : 0);
     if (order == 1 && !pre.empty() && !dec.empty()) {
       std::vector<std::pair<size_t, size_t>> grp;
       for (size_t i = 0; i < dec.size();) {

@@ -955,7 +955,8 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   }
   AttnPlan plan;
   int rc = attn_build_plan(T, B, s->lengths, s->extents, s->pages, s->max_pages, m.block,
-                           c->kv_positions, m.heads, m.kv_heads, plan, c->cascade);
+                           c->kv_positions, m.heads, m.kv_heads, plan, c->cascade,
+                           c->precision == 1);
   if (rc) return rc;
   int pad = -1;
   for (int b = 0; b < B; b++)
@@ -1254,7 +1255,7 @@ int tgohip_paged_attention(tgohip_ctx* c, const void* q, int q_dtype, int T, int
     return fail(TGOHIP_EINVAL, "attention: the cache view exceeds 32-bit element offsets");
   AttnPlan plan;
   int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan,
-                           c->cascade);
+                           c->cascade, q_dtype != TGOHIP_F16);
   if (rc) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
   Stager sg;
@@ -1283,7 +1284,7 @@ int tgohip_paged_attention_replay(tgohip_ctx* c, const void* q, int q_dtype, int
                                   void* out, int out_dtype, int iters) {
   AttnPlan plan;
   int rc = attn_build_plan(T, B, lengths, extents, pages, max_pages, block, capacity, H, H_kv, plan,
-                           c->cascade);
+                           c->cascade, q_dtype != TGOHIP_F16);
   if (rc) return rc;
   if ((rc = ensure_attn_parts(c, plan.parts))) return rc;
   Stager sg;
