@@ -36,13 +36,13 @@ def new_ctx(torch, form=3, seed=21):
     return ctx
 
 
-def packed_step(rng, rows_pad):
-    """Three members (a prefill chunk, a decode, an idle one) packed by NewBatchStep, plus
-    rows_pad padding rows."""
+def packed_step(rng, rows_pad, shape=((13, 13), (0, 0), (9, 1))):
+    """Members (by default a prefill chunk, an idle one and a decode; (prompt, new) tokens
+    each) packed by NewBatchStep, plus rows_pad padding rows."""
     c = CFG
     pool = host.Pool(c["block"], c["positions"] // c["block"])
     members = []
-    for n_prompt, n_new in ((13, 13), (0, 0), (9, 1)):
+    for n_prompt, n_new in shape:
         if n_prompt == 0:
             members.append(host.Member([], 0, []))
             continue
@@ -73,6 +73,30 @@ def test_derived_ports_equal_the_packed_ports(torch_gpu, rows_pad):
     assert not la[1].any() and aa[1] == -1
     assert la[0].any() and la[2].any() and aa[0] >= 0 and aa[2] >= 0
     # the KV pools the two steps wrote, every layer (padding rows write nothing)
+    torch.cuda.synchronize()
+    pools = [pool_copy(x) for x in (a, b)]
+    assert np.array_equal(pools[0], pools[1])
+    assert np.count_nonzero(pools[0]) > 0
+    a.close()
+    b.close()
+
+
+def test_fused_qkv_epilogue_equals_the_separate_kernel(torch_gpu):
+    """69 rows (a 48-token chunk, an idle member, a decode, a 20-token chunk after 10 cached
+    positions): the QKV projection runs on the pipelined exact kernel, unsplit with one k
+    group (K = 256), so with derived rows it does q/k-norm, RoPE and the K/V write in its
+    epilogue, while packed ports take the separate qk_rope_kv_kernel. Both compute every
+    value the same way: logits, tokens and both KV pools equal to the bit."""
+    torch = torch_gpu
+    st, table, max_pages = packed_step(np.random.default_rng(9), 0,
+                                       ((48, 48), (0, 0), (9, 1), (30, 20)))
+    assert len(st["ids"]) == 69
+    a, b = new_ctx(torch), new_ctx(torch)
+    la, aa, _ = a.step(st, table, max_pages)
+    lb, ab, _ = b.step(dict(st, posq=None, posk=None, slots=None), table, max_pages)
+    assert np.isfinite(la).all() and la[0].any() and la[3].any()
+    assert np.array_equal(la, lb)
+    assert np.array_equal(aa, ab)
     torch.cuda.synchronize()
     pools = [pool_copy(x) for x in (a, b)]
     assert np.array_equal(pools[0], pools[1])

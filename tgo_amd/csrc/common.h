@@ -85,8 +85,11 @@ struct AttnPlan {
 
 // ---- GEMM (kernels/gemm.hip) --------------------------------------------
 // EPI_SWIGLU_X2 stores the SwiGLU output as an activation pair (below).
+// EPI_QKROPE (the exact pipelined kernel, unsplit, derived rows): the QKV
+// projection's q/k-norm, RoPE and K/V write run in its epilogue, as
+// qk_rope_kv_kernel would run them on its output (qk_head_row below).
 enum { EPI_F32 = 0, EPI_F16 = 1, EPI_RESID = 2, EPI_SWIGLU_F16 = 3, EPI_SWIGLU_F32 = 4,
-       EPI_SWIGLU_X2 = 5 };
+       EPI_SWIGLU_X2 = 5, EPI_QKROPE = 6 };
 // How an activation [M][K] is stored for a projection:
 //   XK_F16  f16, rounded once (the fast f16 path, precision mode 0);
 //   XK_F32  f32 (tgo's arithmetic; split into f16 hi + lo inside the kernel);
@@ -171,6 +174,72 @@ struct QKRopeArgs {
   int q_f16;
   const float4_t* rope;   // [T][32] (rope_table), or null: the kernel computes the angles
 };
+
+// Sum over the 32 lanes of a half wave (lanes 0-31 and 32-63 separately).
+__device__ __forceinline__ float qk_half_wave_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One head row hh of row t (nn/attention.go:192-232), the lane's dims
+// 4*l32 .. 4*l32+3 of it in v: a value head is narrowed and scattered to
+// slot; a q or k head is RMS-normalized over its 128 dims (the half wave
+// sums the squares), scaled by its gain, rotated in interleaved pairs by
+// (c0, s0) and (c1, s1), and stored (q to a.q, k narrowed to slot). A slot at
+// or past capacity writes nothing. angles(pos) gives (c0, s0, c1, s1) for the
+// head's position, called only for q and k heads. qk_rope_kv_kernel and the
+// QKV projection's fused epilogue both call this, so both compute the same
+// values from the same projection output.
+template <typename Angles>
+__device__ __forceinline__ void qk_head_row(const QKRopeArgs& a, int t, int hh, int l32, float4_t v,
+                                            uint32_t slot, Angles angles) {
+  constexpr int kHD = 128;
+  const bool write = slot < (uint32_t)a.capacity;
+  if (hh >= a.H + a.Hkv) {
+    if (write) {
+      const int vh = hh - a.H - a.Hkv;
+      const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+      *(half4_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHD + 4 * l32) = hv;
+    }
+    return;
+  }
+  const bool isq = hh < a.H;
+  const float* gain = isq ? a.qnorm : a.knorm;
+  // The fused multiply-adds are written out (in the order the compiler chose
+  // for qk_rope_kv_kernel when it contracted the expressions itself), so
+  // every kernel that inlines this computes the same bits: left to
+  // contraction, x0 s0 + x1 c0 became fma(x1, c0, x0 s0) in one kernel and
+  // fma(s0, x0, x1 c0) in another.
+  const float ss = qk_half_wave_sum(
+      __builtin_fmaf(v[3], v[3], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[0], v[0], v[1] * v[1]))));
+  const float sc = 1.0f / sqrtf(ss / (float)kHD + a.eps);
+  const float4_t g = *(const float4_t*)(gain + 4 * l32);
+  const float x0 = v[0] * sc * g[0], x1 = v[1] * sc * g[1];
+  const float x2 = v[2] * sc * g[2], x3 = v[3] * sc * g[3];
+  float c0, s0, c1, s1;
+  angles(isq, hh, c0, s0, c1, s1);
+  const float y0 = __builtin_fmaf(x0, c0, -(x1 * s0)), y1 = __builtin_fmaf(x1, c0, x0 * s0);
+  const float y2 = __builtin_fmaf(x2, c1, -(x3 * s1)), y3 = __builtin_fmaf(x3, c1, x2 * s1);
+  if (isq && a.q_f16) {
+    const half4_t hq = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+    *(half4_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHD + 4 * l32) = hq;
+  } else if (isq) {
+    *(float4_t*)((float*)a.q + ((size_t)t * a.H + hh) * kHD + 4 * l32) = float4_t{y0, y1, y2, y3};
+  } else if (write) {
+    const int kh = hh - a.H;
+    const half4_t hk = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+    *(half4_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHD + 4 * l32) = hk;
+  }
+}
+
+// The QKV projection of an activation pair [M][K] with qk_head_row in its
+// epilogue (EPI_QKROPE) instead of an f32 output for qk_rope_kv_kernel: when
+// gemm_qkrope_fusable, gemm_enqueue_qkrope does both in one launch (qa as
+// for qk_rope_kv_kernel, with rope set; qkv and the split fields unused).
+bool gemm_qkrope_fusable(const PackedWeight& w, int M, int ncu);
+int gemm_enqueue_qkrope(const PackedWeight& w, const void* x, int M, const QKRopeArgs& qa, int ncu,
+                        hipStream_t st);
 // ids[t] with bit 31 set names a member b = ids[t] & 0x7fffffff whose token is
 // feed[b] (the previous step's argmax, left on the device).
 void launch_embed(const uint32_t* ids, int T, const void* table, const uint16_t* scales, int form,

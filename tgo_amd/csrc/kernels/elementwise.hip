@@ -198,13 +198,6 @@ __global__ __launch_bounds__(256) void derive_rows_kernel(DeriveArgs a) {
   }
 }
 
-// Sum over the 32 lanes of a half wave (lanes 0-31 and 32-63 separately).
-__device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 // One block (4 waves) per token. A wave takes two head rows at a time (lanes
 // 0-31 head 2k, lanes 32-63 head 2k+1, wave w taking k = w, w+4, ...); a lane
 // owns four consecutive dims, the rotated pairs (4l, 4l+1) and (4l+2, 4l+3),
@@ -217,7 +210,6 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
   const int W = NH * kHeadDim;
   const uint32_t slot = a.slots[t];
   const int dpos = a.rowpos ? (int)a.rowpos[t] : 0;  // the row's position when derived
-  const bool write = slot < (uint32_t)a.capacity;
   int cpos = -1;
   float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
   const double inv0 = a.inv_freq[2 * l32], inv1 = a.inv_freq[2 * l32 + 1];
@@ -242,46 +234,24 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKRopeArgs a) {
     } else {
       v = sum_planes(a.qkv, a.nsplit, a.plane, off);
     }
-    if (hh >= a.H + a.Hkv) {
-      // value head: narrowed and scattered as is
-      if (write) {
-        const int vh = hh - a.H - a.Hkv;
-        const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-        *(half4_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHeadDim + 4 * l32) = hv;
+    qk_head_row(a, t, hh, l32, v, slot, [&](bool isq, int h2, float& cc0, float& ss0, float& cc1,
+                                             float& ss1) {
+      const int pos = a.rowpos ? dpos
+                      : isq   ? (int)a.posq[(size_t)t * a.H + h2]
+                              : (int)a.posk[(size_t)t * a.Hkv + (h2 - a.H)];
+      if (pos != cpos) {
+        const double ang0 = (double)pos * inv0, ang1 = (double)pos * inv1;
+        c0 = (float)cos(ang0);
+        s0 = (float)sin(ang0);
+        c1 = (float)cos(ang1);
+        s1 = (float)sin(ang1);
+        cpos = pos;
       }
-      continue;
-    }
-    const bool isq = hh < a.H;
-    const float* gain = isq ? a.qnorm : a.knorm;
-    const float ss = half_wave_sum(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
-    const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
-    const float4_t g = *(const float4_t*)(gain + 4 * l32);
-    const float x0 = v[0] * sc * g[0], x1 = v[1] * sc * g[1];
-    const float x2 = v[2] * sc * g[2], x3 = v[3] * sc * g[3];
-    const int pos = a.rowpos ? dpos
-                    : isq   ? (int)a.posq[(size_t)t * a.H + hh]
-                            : (int)a.posk[(size_t)t * a.Hkv + (hh - a.H)];
-    if (pos != cpos) {
-      const double ang0 = (double)pos * inv0, ang1 = (double)pos * inv1;
-      c0 = (float)cos(ang0);
-      s0 = (float)sin(ang0);
-      c1 = (float)cos(ang1);
-      s1 = (float)sin(ang1);
-      cpos = pos;
-    }
-    const float y0 = x0 * c0 - x1 * s0, y1 = x0 * s0 + x1 * c0;
-    const float y2 = x2 * c1 - x3 * s1, y3 = x2 * s1 + x3 * c1;
-    if (isq && a.q_f16) {
-      const half4_t hq = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-      *(half4_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) = hq;
-    } else if (isq) {
-      *(float4_t*)((float*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) =
-          float4_t{y0, y1, y2, y3};
-    } else if (write) {
-      const int kh = hh - a.H;
-      const half4_t hk = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-      *(half4_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHeadDim + 4 * l32) = hk;
-    }
+      cc0 = c0;
+      ss0 = s0;
+      cc1 = c1;
+      ss1 = s1;
+    });
   }
 }
 

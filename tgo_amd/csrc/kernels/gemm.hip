@@ -630,7 +630,7 @@ __device__ __forceinline__ void pipe_bfrag_x(const PipeB<TGOHIP_FORM_I8>& r, int
 // (2^-22 relative) dropped as in the three-MFMA form.
 template <int FORM, int EPI, int MW, int NW, int KQ = 1, bool EX = false>
 __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_kernel(
-    GemmArgs g, int tiles_n, int tiles, int colmajor, int xsplit) {
+    GemmArgs g, int tiles_n, int tiles, int colmajor, int xsplit, QKRopeArgs qa) {
   constexpr int MB = MW / 32;
   constexpr bool FX = EX && FORM == TGOHIP_FORM_I4_SYM;  // factored scales
   constexpr int ACH = MW / (8 * NW);  // 1 KiB LDS-DMA chunks per wave per k-step and plane
@@ -994,7 +994,47 @@ __global__ __launch_bounds__((64 * NW * KQ), (8 / (NW * KQ))) void gemm_pipe_ker
           for (int e = 0; e < 4; e++) acc[mb][b][4 * r4 + e] += o[e];
         }
   }
-  gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, nsplit > 1, split);
+  if constexpr (EPI == EPI_QKROPE) {
+    // The tile (64 rows x two 128-wide heads; the host launches this only
+    // unsplit, with one k group, 64-row tiles and whole heads per tile) goes
+    // through LDS, rows 16i..16i+15 in stage i of the A ring, so that each
+    // half wave can take a head row with four consecutive dims per lane, as
+    // qk_rope_kv_kernel does; the angles come from the step's rope table.
+    static_assert(MW == 64 && NW == 4 && KQ == 1, "one 64 x 256 f32 tile fills the A ring");
+    __syncthreads();  // every wave's last ring reads are done (its DMAs waited above)
+    // (a stage picked by value: an array of the stages' addresses would need
+    // a static initializer)
+    auto ring = [](int i, half_t* s0, half_t* s1, half_t* s2, half_t* s3) {
+      return (float*)(i == 0 ? s0 : i == 1 ? s1 : i == 2 ? s2 : s3);
+    };
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          ring(row >> 4, As0, As1, As2, As3)[(row & 15) * 256 + wave * 64 + b * 32 + c32] = acc[mb][b][r];
+        }
+    __syncthreads();
+    // wave w takes rows w, w + 4, ...; its half waves the tile's two heads
+    for (int row = wave; row < MW; row += NW) {
+      const int t = m0 + row;
+      if (t >= g.M) break;  // wave-uniform
+      const float4_t v =
+          *(const float4_t*)(ring(row >> 4, As0, As1, As2, As3) + (row & 15) * 256 + h * 128 + 4 * c32);
+      const float4_t cs = qa.rope[(size_t)t * 32 + c32];
+      qk_head_row(qa, t, 2 * tn + h, c32, v, qa.slots[t],
+                  [&](bool, int, float& c0, float& s0, float& c1, float& s1) {
+                    c0 = cs[0];
+                    s0 = cs[1];
+                    c1 = cs[2];
+                    s1 = cs[3];
+                  });
+    }
+  } else {
+    gemm_epilogue<EPI, MB>(g, acc, m0, nbw0, nbv, h, c32, nsplit > 1, split);
+  }
 #undef PIPE_DMA_A
 }
 
@@ -1680,10 +1720,10 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
 
 template <int FORM, int MW, int NW, int KQ = 1, bool EX = false>
 static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n, int tiles,
-                             int cm, int xs, hipStream_t st) {
+                             int cm, int xs, const QKRopeArgs& qa, hipStream_t st) {
   const dim3 blk(64 * NW * KQ);
 #define PIPE_LAUNCH(E) \
-  hipLaunchKernelGGL((gemm_pipe_kernel<FORM, E, MW, NW, KQ, EX>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs)
+  hipLaunchKernelGGL((gemm_pipe_kernel<FORM, E, MW, NW, KQ, EX>), grid, blk, 0, st, g, tiles_n, tiles, cm, xs, qa)
   switch (epi) {
     case EPI_F32: PIPE_LAUNCH(EPI_F32); break;
     case EPI_F16: PIPE_LAUNCH(EPI_F16); break;
@@ -1691,19 +1731,21 @@ static void launch_pipe_form(const GemmArgs& g, int epi, dim3 grid, int tiles_n,
     case EPI_SWIGLU_F16: if constexpr (!EX) PIPE_LAUNCH(EPI_SWIGLU_F16); break;
     case EPI_SWIGLU_F32: if constexpr (!EX) PIPE_LAUNCH(EPI_SWIGLU_F32); break;
     case EPI_SWIGLU_X2: if constexpr (EX) PIPE_LAUNCH(EPI_SWIGLU_X2); break;
+    case EPI_QKROPE: if constexpr (EX && MW == 64 && NW == 4 && KQ == 1) PIPE_LAUNCH(EPI_QKROPE); break;
   }
 #undef PIPE_LAUNCH
 }
 
 template <int FORM>
 static void launch_pipe_shape(const GemmArgs& g, int epi, dim3 grid, int mw, int nw, int kq,
-                              int tiles_n, int tiles, int cm, int xs, bool ex, hipStream_t st) {
-  if (ex && kq == 2) launch_pipe_form<FORM, 64, 4, 2, true>(g, epi, grid, tiles_n, tiles, cm, xs, st);
-  else if (ex) launch_pipe_form<FORM, 64, 4, 1, true>(g, epi, grid, tiles_n, tiles, cm, xs, st);
-  else if (mw == 64 && kq == 2) launch_pipe_form<FORM, 64, 4, 2>(g, epi, grid, tiles_n, tiles, cm, xs, st);
-  else if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
-  else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, cm, xs, st);
-  else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, cm, xs, st);
+                              int tiles_n, int tiles, int cm, int xs, bool ex, const QKRopeArgs& qa,
+                              hipStream_t st) {
+  if (ex && kq == 2) launch_pipe_form<FORM, 64, 4, 2, true>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
+  else if (ex) launch_pipe_form<FORM, 64, 4, 1, true>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
+  else if (mw == 64 && kq == 2) launch_pipe_form<FORM, 64, 4, 2>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
+  else if (mw == 64) launch_pipe_form<FORM, 64, 4>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
+  else if (nw == 8) launch_pipe_form<FORM, 128, 8>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
+  else launch_pipe_form<FORM, 128, 4>(g, epi, grid, tiles_n, tiles, cm, xs, qa, st);
 }
 
 // TGOHIP_GEMM_KQ=0 keeps one k group in every workgroup.
@@ -1739,7 +1781,7 @@ static PipeLaunch pipe_launch(const PackedWeight& w, int M, int ncu, int epi, bo
 // xlo: the lo plane of an XK_X2 activation (the exact kernel), or null.
 static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, const void* xlo, int M, void* y,
                              int epi, float* workspace, size_t ws_bytes, int ncu, hipStream_t st,
-                             int* defer) {
+                             int* defer, const QKRopeArgs* qa = nullptr) {
   const bool ex = xlo != nullptr;
   const PipeLaunch pl = pipe_launch(w, M, ncu, epi, ex);
   const int mw = pl.mw, nw = pl.nw, tiles_n = pl.tiles_n, tiles = pl.tiles, kq = pl.kq;
@@ -1772,13 +1814,13 @@ static int gemm_pipe_enqueue(const PackedWeight& w, const void* x, const void* x
   const int cm = tiles / tiles_n <= 4 ? 1 : 0;
   switch (w.form) {
     case TGOHIP_FORM_I4_SYM:
-      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_SYM>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, qa ? *qa : QKRopeArgs{}, st);
       break;
     case TGOHIP_FORM_I4_TGO:
-      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
+      launch_pipe_shape<TGOHIP_FORM_I4_TGO>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, qa ? *qa : QKRopeArgs{}, st);
       break;
     default:
-      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, st);
+      launch_pipe_shape<TGOHIP_FORM_I8>(g, epi, grid, mw, nw, kq, tiles_n, tiles, cm, xs, ex, qa ? *qa : QKRopeArgs{}, st);
       break;
   }
   if (defer) *defer = splits > 1 ? splits : 0;
@@ -1825,6 +1867,24 @@ size_t gemm_workspace_bytes(const PackedWeight& w, int M, int ncu, int xk) {
     s = choose_splits(M, w.N, w.K, MW, ncu);  // gemm_kernel's grid.z
   }
   return s > 1 ? (size_t)s * split_plane_stride(M, w.N) * sizeof(float) : 0;
+}
+
+// The QKV projection with q/k-norm, RoPE and the K/V write in its epilogue
+// (EPI_QKROPE): an activation pair on the pipelined exact kernel, unsplit,
+// one k group per workgroup, whole 128-wide heads in each 256-column tile,
+// and a rope table for the rows.
+bool gemm_qkrope_fusable(const PackedWeight& w, int M, int ncu) {
+  if (M <= 0 || !use_pipe(w, XK_X2, M) || w.N % 256 != 0) return false;
+  const PipeLaunch pl = pipe_launch(w, M, ncu, EPI_F32, true);
+  return pl.splits == 1 && pl.kq == 1 && pl.mw == 64 && pl.nw == 4;
+}
+
+int gemm_enqueue_qkrope(const PackedWeight& w, const void* x, int M, const QKRopeArgs& qa, int ncu,
+                        hipStream_t st) {
+  if (!gemm_qkrope_fusable(w, M, ncu) || !qa.rope || w.N != (qa.H + 2 * qa.Hkv) * 128)
+    return fail(TGOHIP_ESTATE, "linear: the fused QKV epilogue does not apply to this launch");
+  const void* xlo = (const half_t*)x + (size_t)M * w.K;
+  return gemm_pipe_enqueue(w, x, xlo, M, nullptr, EPI_QKROPE, nullptr, 0, ncu, st, nullptr, &qa);
 }
 
 int gemm_enqueue(const PackedWeight& w, const void* x, int xk, int M, void* y, int epi,

@@ -1096,24 +1096,42 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
   // rmsnorm. `pend` counts the planes of a residual add still owed to h.
   const size_t plane = split_plane_stride(Tw, m.hidden);
   int pend = 0;
+  // tgo's arithmetic with device-derived rows: the QKV projection runs its
+  // q/k-norm, RoPE and K/V write in its epilogue where its launch allows
+  // (unsplit; at the C4 step's 1152 rows, not at 128); TGOHIP_FUSE_QK=0 keeps
+  // the separate kernel. Both compute the same values.
+  static const bool fuse_env = [] {
+    const char* e = getenv("TGOHIP_FUSE_QK");
+    return !(e && atoi(e) == 0);
+  }();
+  const bool fuse_qk = fuse_env && f32act && derived && c->layers.size() > 0 &&
+                       gemm_qkrope_fusable(c->layers[0].qkv, Tw, c->ncu);
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
     launch_rmsnorm(h, nullptr, Tw, L.g_attn, m.hidden, m.rms_eps, c->xn.p, outf, st, ws, pend, plane);
     int qkv_split = 0;
-    if ((rc = mark(TGOHIP_PROF_QKV, l, 0))) return rc;
-    if ((rc = gemm_enqueue(L.qkv, c->xn.p, xk, Tw, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
-                           &qkv_split)))
-      return rc;
-    if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
-    QKRopeArgs qa{qkv_split ? ws : (const float*)c->qkv.p, qkv_split,
-                  split_plane_stride(Tw, (m.heads + 2 * m.kv_heads) * kHeadDim), L.g_q, L.g_k,
+    QKRopeArgs qa{nullptr, 0, split_plane_stride(Tw, (m.heads + 2 * m.kv_heads) * kHeadDim),
+                  L.g_q, L.g_k,
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posq),
                   derived ? nullptr : sg.dev<uint32_t>(c, o_posk),
                   derived ? d_rowslot : sg.dev<uint32_t>(c, o_slots), derived ? d_rowpos : nullptr,
                   c->inv_freq, c->q.p, c->kc + l * layer_kv,
                   c->vc + l * layer_kv, m.heads, m.kv_heads, c->kv_positions, m.rms_eps, qf16,
                   derived ? (const float4_t*)c->rope.p : nullptr};
-    launch_qk_rope_kv(qa, Tw, st);
+    if ((rc = mark(TGOHIP_PROF_QKV, l, 0))) return rc;
+    if (fuse_qk) {
+      // q/k-norm, RoPE and the K/V write in the projection's epilogue
+      if ((rc = gemm_enqueue_qkrope(L.qkv, c->xn.p, Tw, qa, c->ncu, st))) return rc;
+      if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
+    } else {
+      if ((rc = gemm_enqueue(L.qkv, c->xn.p, xk, Tw, c->qkv.p, EPI_F32, ws, wsb, c->ncu, st,
+                             &qkv_split)))
+        return rc;
+      if ((rc = mark(TGOHIP_PROF_QKV, l, 1))) return rc;
+      qa.qkv = qkv_split ? ws : (const float*)c->qkv.p;
+      qa.nsplit = qkv_split;
+      launch_qk_rope_kv(qa, Tw, st);
+    }
     if ((rc = mark(TGOHIP_PROF_ATTN, l, 0))) return rc;
     if ((rc = attn_enqueue(plan, dp, c->q.p, qf16, c->kc + l * layer_kv, c->vc + l * layer_kv, c->attn.p,
                            outf, Tw, m.heads, m.kv_heads, s->max_pages, m.block, scale, st)))
