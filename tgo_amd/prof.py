@@ -146,7 +146,8 @@ XCDS = 8      # GRBM_GUI_ACTIVE is reported summed over the XCDs
 
 def label_projections(names):
     """The projection each GEMM dispatch computes, from the step's launch order: per layer
-    rmsnorm, QKV, qk_rope_kv, attention (+ combine), O, rmsnorm, gate/up, down; after the
+    rmsnorm, QKV, qk_rope_kv (unless the QKV epilogue does its work), attention (+ combine),
+    O, rmsnorm, gate/up, down; after the
     last layer a gathered rmsnorm and the LM head, followed by the greedy selection
     (argmax_part_kernel; zero_idle_rows_kernel in traces of earlier builds)."""
     labels = [None] * len(names)
