@@ -330,6 +330,37 @@ def test_small_m_kernel_against_its_operands(ctx, torch_gpu, KN):
         ctx.weight_free(h)
 
 
+@pytest.mark.parametrize("M", [33, 131, 1152])
+@pytest.mark.parametrize("KN", [(2048, 416), (512, 3712)])
+@pytest.mark.parametrize("form", [3, 2, 1])
+def test_large_m_exact_ragged_edges(ctx, torch_gpu, M, KN, form):
+    """The pipelined exact path (activation pairs, tgo's arithmetic; symmetric int4 with its
+    group scale applied in f32, the other forms with the exact weight pair) at partial row
+    and column tiles: N = 416 and 3712 leave the last 256-column tile 160 and 128 columns
+    wide; K = 2048 at 33 and 131 rows splits K. Every column against the f64 product of the
+    f32 activations and the oracle's f32 dequantized weights, AccumF32 + 2^-22."""
+    torch = torch_gpu
+    import tgo_amd
+    K, N = KN
+    if form == 2 and N % 128:
+        N = 512  # tgo's int4 groups run along N in 128s
+    wd, _ = make_weight(form, K, N, np.random.default_rng(29 + M))
+    w64 = torch.from_numpy(deq(form, K, N, wd).astype(np.float64)).cuda()
+    h = ctx.weight_upload(form, K, N, wd["plane"], wd.get("scales"), wd.get("zeros"))
+    try:
+        x = torch.randn(M, K, device="cuda")
+        hi = x.half()
+        lo = (x - hi.float()).half()
+        y = torch.full((M, N), float("nan"), device="cuda")
+        ctx.linear(h, torch.cat([hi.reshape(-1), lo.reshape(-1)]), M, y, x_dtype=tgo_amd.F16X2)
+        torch.cuda.synchronize()
+        ref = x.double() @ w64
+        tol = (4 * (K ** 0.5) * 2.0 ** -24 + 2.0 ** -22) * (x.double().abs() @ w64.abs())
+        assert bool(((y.double() - ref).abs() <= tol).all())
+    finally:
+        ctx.weight_free(h)
+
+
 @pytest.mark.parametrize("M", [33, 47, 96, 131, 300, 1000, 1152])
 @pytest.mark.parametrize("KN", [(2048, 416), (512, 4096), (512, 3712)])
 @pytest.mark.parametrize("form", [3, 2, 1])
