@@ -1104,10 +1104,11 @@ int step_launch(tgohip_ctx* c, const tgohip_batch_step* s, StepLaunch& o) {
     const char* e = getenv("TGOHIP_FUSE_QK");
     return !(e && atoi(e) == 0);
   }();
-  const bool fuse_qk = fuse_env && f32act && derived && c->layers.size() > 0 &&
-                       gemm_qkrope_fusable(c->layers[0].qkv, Tw, c->ncu);
+  const bool fuse_ok = fuse_env && f32act && derived;
   for (int l = 0; l < m.layers; l++) {
     const Layer& L = c->layers[l];
+    // per layer: a checkpoint's layers may hold different weight forms
+    const bool fuse_qk = fuse_ok && gemm_qkrope_fusable(L.qkv, Tw, c->ncu);
     launch_rmsnorm(h, nullptr, Tw, L.g_attn, m.hidden, m.rms_eps, c->xn.p, outf, st, ws, pend, plane);
     int qkv_split = 0;
     QKRopeArgs qa{nullptr, 0, split_plane_stride(Tw, (m.heads + 2 * m.kv_heads) * kHeadDim),
