@@ -23,6 +23,7 @@ def weight(ctx, form, K, N, seed):
     (tgo_amd.FORM_I8, 4096, 6144, (64, 48), tgo_amd.F16),          # 8 splits both
     (tgo_amd.FORM_F16, 4096, 4096, (200, 33), tgo_amd.F32),       # gemm_kernel, 16 splits, f32 x
     (tgo_amd.FORM_I4_TGO, 4096, 12288, (130, 65), tgo_amd.F16),    # 3 then 4 splits
+    (tgo_amd.FORM_I4_SYM, 4096, 4096, (128, 64), tgo_amd.F16X2),   # exact kernel, 8 splits both
 ])
 def test_noalloc_linear_equals_linear(ctx, torch_gpu, form, K, N, Ms, xf):
     torch = torch_gpu
@@ -33,7 +34,11 @@ def test_noalloc_linear_equals_linear(ctx, torch_gpu, form, K, N, Ms, xf):
             assert ctx.linear_workspace(h, M, x_dtype=xf) > 0, "this call should split K"
             g = torch.Generator(device="cuda").manual_seed(M)
             x = torch.randn(M, K, device="cuda", generator=g)
-            x = x.half() if xf == tgo_amd.F16 else x
+            if xf == tgo_amd.F16:
+                x = x.half()
+            elif xf == tgo_amd.F16X2:  # the activation pair: f16 hi plane, then lo plane
+                hi = x.half()
+                x = torch.cat([hi.reshape(-1), (x - hi.float()).half().reshape(-1)])
             want = torch.full((M, N), float("nan"), device="cuda")
             got = torch.full((M, N), float("nan"), device="cuda")
             ctx.linear(h, x, M, want, x_dtype=xf)
