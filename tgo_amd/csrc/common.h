@@ -194,13 +194,12 @@ __device__ __forceinline__ float qk_half_wave_sum(float v) {
 template <typename Angles>
 __device__ __forceinline__ void qk_head_row(const QKRopeArgs& a, int t, int hh, int l32, float4_t v,
                                             uint32_t slot, Angles angles) {
-  constexpr int kHD = 128;
   const bool write = slot < (uint32_t)a.capacity;
   if (hh >= a.H + a.Hkv) {
     if (write) {
       const int vh = hh - a.H - a.Hkv;
       const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-      *(half4_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHD + 4 * l32) = hv;
+      *(half4_t*)(a.vc + ((size_t)slot * a.Hkv + vh) * kHeadDim + 4 * l32) = hv;
     }
     return;
   }
@@ -213,7 +212,7 @@ __device__ __forceinline__ void qk_head_row(const QKRopeArgs& a, int t, int hh, 
   // fma(s0, x0, x1 c0) in another.
   const float ss = qk_half_wave_sum(
       __builtin_fmaf(v[3], v[3], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[0], v[0], v[1] * v[1]))));
-  const float sc = 1.0f / sqrtf(ss / (float)kHD + a.eps);
+  const float sc = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
   const float4_t g = *(const float4_t*)(gain + 4 * l32);
   const float x0 = v[0] * sc * g[0], x1 = v[1] * sc * g[1];
   const float x2 = v[2] * sc * g[2], x3 = v[3] * sc * g[3];
@@ -223,13 +222,13 @@ __device__ __forceinline__ void qk_head_row(const QKRopeArgs& a, int t, int hh, 
   const float y2 = __builtin_fmaf(x2, c1, -(x3 * s1)), y3 = __builtin_fmaf(x3, c1, x2 * s1);
   if (isq && a.q_f16) {
     const half4_t hq = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-    *(half4_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHD + 4 * l32) = hq;
+    *(half4_t*)((half_t*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) = hq;
   } else if (isq) {
-    *(float4_t*)((float*)a.q + ((size_t)t * a.H + hh) * kHD + 4 * l32) = float4_t{y0, y1, y2, y3};
+    *(float4_t*)((float*)a.q + ((size_t)t * a.H + hh) * kHeadDim + 4 * l32) = float4_t{y0, y1, y2, y3};
   } else if (write) {
     const int kh = hh - a.H;
     const half4_t hk = {(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-    *(half4_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHD + 4 * l32) = hk;
+    *(half4_t*)(a.kc + ((size_t)slot * a.Hkv + kh) * kHeadDim + 4 * l32) = hk;
   }
 }
 
