@@ -1710,8 +1710,9 @@ static void pipe_shape(const PackedWeight& w, int M, int ncu, int& mw, int& nw, 
   }
   // A SwiGLU launch over half the CUs or more stays whole (the reduction
   // would apply the epilogue), except an exact one under 80% of a round: the
-  // C4 gate/up at 128 rows (192 tiles, two k groups on 192 of 256 CUs) takes
-  // 4 splits and the reduction, 74 -> 64.5 us with it.
+  // C4 gate/up at 128 rows (192 tiles: whole, two k groups on 192 of 256
+  // CUs) keeps the 2 splits of a launch under half the slots, with the
+  // reduction, 74 -> 64.5 us (forced to 3, 4, 6 or 8 splits: 68-80 us).
   if ((epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) && tiles >= ncu / 2 &&
       !(ex && 5 * tiles < 4 * ncu * (8 / nw)))
     splits = 1;
