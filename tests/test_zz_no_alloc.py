@@ -3,7 +3,8 @@ static device workspace -- against tgohip_linear, through the C ABI: the same ke
 splits, so the outputs are equal to the bit. Two calls in a row, the second with fewer
 rows, so the second runs on the array the first left behind; every call here splits K
 (tgohip_linear_workspace says so), so both use the array; an empty batch launches nothing;
-a call needing more than the array holds is refused."""
+a call needing more than the array holds is refused; and calls captured into a HIP graph
+replay to the same bits as eager calls."""
 import numpy as np
 import pytest
 
@@ -78,5 +79,56 @@ def test_noalloc_linear_empty_batch_launches_nothing(ctx, torch_gpu):
         ctx.linear_noalloc(h, x, 0, y, x_dtype=tgo_amd.F16)
         torch.cuda.synchronize()
         assert bool((y == 7.0).all())
+    finally:
+        ctx.weight_free(h)
+
+
+def test_noalloc_linear_replays_under_graph_capture(ctx, torch_gpu):
+    """The allocation-free linear is meant for code under HIP graph capture. Captured on a
+    torch stream (the library launching there), a graph of two calls -- symmetric int4 over
+    f16 activations and over an activation pair, both 8-way split-K at 128 rows, so both
+    use the static workspace -- is replayed five times, with eager work and a
+    synchronization between replays and new inputs written before each. Every replay's
+    outputs equal an eager tgohip_linear of the same inputs to the bit."""
+    torch = torch_gpu
+    K = N = 4096
+    M = 128
+    h = ctx.weight_synth(tgo_amd.FORM_I4_SYM, K, N, 23, 7, 0.02)
+    try:
+        assert ctx.linear_workspace(h, M, x_dtype=tgo_amd.F16) > 0
+        assert ctx.linear_workspace(h, M, x_dtype=tgo_amd.F16X2) > 0
+        x16 = torch.zeros(M, K, device="cuda").half()
+        xp = torch.zeros(2 * M * K, device="cuda").half()
+        y16 = torch.zeros(M, N, device="cuda")
+        yp = torch.zeros(M, N, device="cuda")
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        ctx.set_stream(s.cuda_stream)
+        try:
+            with torch.cuda.graph(g, stream=s):
+                ctx.linear_noalloc(h, x16, M, y16, x_dtype=tgo_amd.F16)
+                ctx.linear_noalloc(h, xp, M, yp, x_dtype=tgo_amd.F16X2)
+        finally:
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        for rep in range(5):
+            print("graph replay %d" % rep, flush=True)
+            x = torch.randn(M, K, device="cuda", generator=gen)
+            x16.copy_(x.half())
+            hi = x.half()
+            xp.copy_(torch.cat([hi.reshape(-1), (x - hi.float()).half().reshape(-1)]))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            w16 = torch.full((M, N), float("nan"), device="cuda")
+            wp = torch.full((M, N), float("nan"), device="cuda")
+            ctx.linear(h, x16, M, w16, x_dtype=tgo_amd.F16)
+            ctx.linear(h, xp, M, wp, x_dtype=tgo_amd.F16X2)
+            torch.cuda.synchronize()
+            assert torch.isfinite(w16).all() and torch.isfinite(wp).all()
+            assert torch.equal(y16, w16), (rep, (y16 - w16).abs().max().item())
+            assert torch.equal(yp, wp), (rep, (yp - wp).abs().max().item())
+        del g
     finally:
         ctx.weight_free(h)
