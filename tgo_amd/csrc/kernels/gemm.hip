@@ -1090,6 +1090,68 @@ __global__ void gemm_reduce_kernel(GemmArgs g, int splits) {
   }
 }
 
+// gemm_reduce_kernel with four consecutive outputs per thread (the host uses
+// it when the output row is a multiple of 4 wide; a SwiGLU's four then stay
+// in one 32-column block): float4 loads from every split's plane, up to
+// eight splits' loads in flight, each element summed in split order from 0
+// as sum_split_values sums it, so the results are the same to the bit.
+template <int EPI>
+__global__ void gemm_reduce4_kernel(GemmArgs g, int splits) {
+  constexpr bool SW = EPI == EPI_SWIGLU_F16 || EPI == EPI_SWIGLU_F32 || EPI == EPI_SWIGLU_X2;
+  const int outN = SW ? g.N / 2 : g.N;
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= (size_t)g.M * outN) return;
+  const int row = (int)(i / outN), col = (int)(i % outN);
+  auto sum4 = [&](size_t off) {
+    float4_t a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+      const int n = min(splits - s0, 8);
+      float4_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (u < n) v[u] = *(const float4_t*)(g.part + (size_t)(s0 + u) * g.pstride + off);
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (u < n) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) a[e] += v[u][e];
+        }
+    }
+    return a;
+  };
+  if (SW) {
+    const size_t gc = (size_t)row * g.N + (col / 32) * 64 + (col % 32);
+    const float4_t ga = sum4(gc), ua = sum4(gc + 32);
+    float4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = silu_f(ga[e]) * ua[e];
+    if (EPI == EPI_SWIGLU_F32) {
+      *(float4_t*)((float*)g.y + i) = v;
+    } else {
+      const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+      *(half4_t*)((half_t*)g.y + i) = hv;
+      if (EPI == EPI_SWIGLU_X2) {
+        half4_t lv;
+#pragma unroll
+        for (int e = 0; e < 4; e++) lv[e] = (half_t)(v[e] - (float)hv[e]);
+        *(half4_t*)((half_t*)g.y + (size_t)g.M * outN + i) = lv;
+      }
+    }
+  } else {
+    const float4_t a = sum4(i);
+    if (EPI == EPI_F32) {
+      *(float4_t*)((float*)g.y + i) = a;
+    } else if (EPI == EPI_F16) {
+      *(half4_t*)((half_t*)g.y + i) = half4_t{(half_t)a[0], (half_t)a[1], (half_t)a[2], (half_t)a[3]};
+    } else {
+      float4_t y = *(const float4_t*)((float*)g.y + i);
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] += a[e];
+      *(float4_t*)((float*)g.y + i) = y;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // repack: canonical host forms (already on the device) -> fragment-major
 // ---------------------------------------------------------------------------
@@ -1610,6 +1672,18 @@ static void launch_mw(int form, const GemmArgs& g, int epi, dim3 grid, hipStream
 static void launch_reduce(const GemmArgs& g, int epi, int splits, hipStream_t st) {
   const int outN = (epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_X2) ? g.N / 2 : g.N;
   const size_t total = (size_t)g.M * outN;
+  if (outN % 4 == 0 && g.pstride % 4 == 0) {  // four outputs per thread
+    const dim3 rg4((unsigned)((total / 4 + 255) / 256)), rb4(256);
+    switch (epi) {
+      case EPI_F32: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_F32>, rg4, rb4, 0, st, g, splits); break;
+      case EPI_F16: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_F16>, rg4, rb4, 0, st, g, splits); break;
+      case EPI_RESID: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_RESID>, rg4, rb4, 0, st, g, splits); break;
+      case EPI_SWIGLU_F16: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_SWIGLU_F16>, rg4, rb4, 0, st, g, splits); break;
+      case EPI_SWIGLU_F32: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_SWIGLU_F32>, rg4, rb4, 0, st, g, splits); break;
+      case EPI_SWIGLU_X2: hipLaunchKernelGGL(gemm_reduce4_kernel<EPI_SWIGLU_X2>, rg4, rb4, 0, st, g, splits); break;
+    }
+    return;
+  }
   const dim3 rg((unsigned)((total + 255) / 256)), rb(256);
   switch (epi) {
     case EPI_F32: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_F32>, rg, rb, 0, st, g, splits); break;
